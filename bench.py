@@ -1,0 +1,179 @@
+#!/usr/bin/env python3
+"""Decode throughput of the Qwen2-0.5B-shaped 4-bit model on one MI355X.
+
+Workload: 24 layers, hidden 896, 14/2 heads of 64, FFN 4864, vocab 151936, tied
+embedding; projections and LM head 4-bit with one fp16 scale per 32 weights, weights
+N(0, 0.02) from a seeded generator, norms 1.0, q/k/v biases N(0, 0.02), fp16 KV cache,
+RoPE theta 1e6. Each sequence gets a 32-token random prompt (prefilled), then greedy
+decode steps (embedding, 24 layers, LM head, repetition penalty, argmax) are replayed
+from a HIP graph. `value` is decode tokens/s at batch 1; the same line carries batch 32.
+
+A step is one decode step of the batch (one token per sequence). Inputs and weights are
+resident in HBM before the timed region.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+METRIC = "decode tok/s @ bs1 & bs32 (Qwen2-0.5B, 4-bit); achieved HBM GB/s vs peak"
+HBM_PEAK = 8.0e12
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def build_model(plane, batch, prompt_len, steps_total, seed=0):
+    import numpy as np
+
+    from bramha_amd import BH_Q4_G32
+    from bramha_amd.model import QWEN2_0_5B, DecoderConfig, HipDecoder, synth_tokens, synth_weights
+
+    cap = prompt_len + steps_total + 8
+    cfg = DecoderConfig(**QWEN2_0_5B, wfmt=BH_Q4_G32, head_fmt=BH_Q4_G32, kv_f16=True, max_seqs=batch,
+                        kv_rows=cap * batch, max_tokens=max(64, batch))
+    m = HipDecoder(plane, cfg)
+    m.load(synth_weights(cfg, seed=seed))
+    firsts = []
+    for s in range(batch):
+        p = synth_tokens(seed, "prompt.%d" % s, prompt_len, cfg.vocab)
+        m.seq_open(s, cap)
+        m.prefill(s, p[:-1])
+        firsts.append(int(p[-1]))
+    m.decode_setup(np.arange(batch, dtype=np.int32), np.array(firsts, np.uint32))
+    return m, cfg
+
+
+def timed_decode(m, steps, warmup):
+    import torch
+
+    m.decode(warmup)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    m.decode(steps)
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0
+
+
+def roofline(m, n_steps=16):
+    """Per-kernel-class mean launch durations over eager decode steps (HIP events on the
+    model's stream) and the algorithmic bytes of one launch; the dominant class is the one
+    with the largest total time per step."""
+    t = m.time_kernels(n_steps)
+    best, best_tot = None, -1.0
+    for k, (mean_us, cnt) in t.items():
+        tot = mean_us * cnt / n_steps
+        if k != "other" and tot > best_tot:
+            best, best_tot = k, tot
+    mean_us = t[best][0]
+    nbytes = m.kernel_bytes(best)
+    achieved = nbytes / (mean_us * 1e-6)
+    return best, {"bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                  "frac": achieved / HBM_PEAK, "traffic": None, "kernel": best, "bytes_per_launch": nbytes,
+                  "mean_us": mean_us,
+                  "per_class_us": {k: round(v[0], 3) for k, v in t.items()},
+                  "launches_per_step": {k: v[1] // n_steps for k, v in t.items()}}
+
+
+def cpu_baseline(budget_s=15.0, max_steps=64):
+    """The reference CPU path (the oracle's restatement of generate_cpu with CPU-only mode):
+    Qwen2-0.5B shape, 4-bit per-row projections (the reference's U4 format) and the f32 tied
+    LM head the reference keeps (cpu_engine.rs:2449-2455), on this host's cores."""
+    import numpy as np
+
+    import oracle
+    from bramha_amd import BH_F32, BH_Q4_ROW
+    from bramha_amd.model import QWEN2_0_5B, DecoderConfig, synth_tokens, synth_weights
+
+    cfg = DecoderConfig(**QWEN2_0_5B, wfmt=BH_Q4_ROW, head_fmt=BH_F32)
+    om = oracle.OracleModel(cfg)
+    om.load(synth_weights(cfg, seed=0))
+    p = synth_tokens(0, "prompt.0", 2, cfg.vocab)
+    om.generate(p, 1)  # warm caches
+    steps = 2
+    while True:
+        t0 = time.perf_counter()
+        n = len(om.generate(p, steps))
+        dt = time.perf_counter() - t0
+        if dt > budget_s / 3 or steps >= max_steps:
+            break
+        steps = min(max_steps, steps * 2)
+    return {"value": n / dt, "unit": "tok/s", "cores": oracle.num_threads(), "kind": "port",
+            "sample": "%d greedy decode steps at batch 1 after a 1-token prefill, 4-bit per-row projections + "
+                      "f32 tied LM head (the reference's CPU 4-bit path), %.1f s" % (n, dt)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--prompt", type=int, default=32)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only-bs1", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: this build runs the decode path on a single MI355X "
+              "(--gpus %d requested). Multi-GPU sharding is described in DESIGN.md, not run." % args.gpus,
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from bramha_amd.plane import HipComputePlane
+
+    plane = HipComputePlane(0)
+    total = args.warmup + args.steps
+    log("building bs1 model")
+    m1, cfg = build_model(plane, 1, args.prompt, total + 32)
+    dt1 = timed_decode(m1, args.steps, args.warmup)
+    tok1 = args.steps / dt1
+    log("bs1: %.1f tok/s (%.3f ms/step)" % (tok1, dt1 * 1e3 / args.steps))
+    kern, roof = roofline(m1)
+    log("dominant kernel %s: %.1f GB/s (%.1f%% of HBM peak)" % (kern, roof["achieved"], 100 * roof["frac"]))
+    m1.close()
+    bs32 = None
+    if not args.only_bs1:
+        log("building bs32 model")
+        m32, _ = build_model(plane, 32, args.prompt, total)
+        dt32 = timed_decode(m32, args.steps, args.warmup)
+        bs32 = {"value": 32 * args.steps / dt32, "unit": "tok/s", "ms_per_step": dt32 * 1e3 / args.steps,
+                "batch": 32}
+        log("bs32: %.1f tok/s (%.3f ms/step)" % (bs32["value"], bs32["ms_per_step"]))
+        m32.close()
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline")
+        cpu = cpu_baseline()
+        log("cpu baseline: %.2f tok/s on %d threads" % (cpu["value"], cpu["cores"]))
+    line = {
+        "metric": METRIC,
+        "value": tok1,
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": dt1 * 1e3 / args.steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "qwen2-0.5b-shape greedy decode, batch 1, 4-bit g32 fp16-scale projections and "
+                               "tied LM head, fp16 KV, 32-token prompt, random-init weights N(0,0.02)",
+                   "batch": 1, "prompt_len": args.prompt, "context_at_end": args.prompt + total,
+                   "layers": cfg.n_layers, "hidden": cfg.hidden, "vocab": cfg.vocab},
+        "bs32": bs32,
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    plane.close()
+    torch.cuda.synchronize()
+
+
+if __name__ == "__main__":
+    main()

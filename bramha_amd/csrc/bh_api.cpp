@@ -1,0 +1,517 @@
+// bh_api.cpp — context, weight registry and single-op entry points of the C ABI.
+//
+// HipComputePlane below is this backend's counterpart of WgpuComputePlane
+// (src/compute/wgpu_backend.rs:100-117): one context per device holding a
+// stream and a registry of device-resident weights keyed "model:layer" with
+// least-recently-used eviction under a byte cap (ModelBuffers, :25-82;
+// get_or_create_op, :603-722). Its matvec_mul* methods keep the reference's
+// argument meaning and error behaviour: empty input -> Ok(zeros), size
+// mismatch -> Err(text), everything else -> Ok(result).
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <list>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "bh_ctx.h"
+
+using namespace bh;
+
+// ------------------------------------------------------------------ helpers
+int bh_ctx::fail(int status, const std::string& msg) {
+    err = msg;
+    return status;
+}
+
+int bh_ctx::hip_fail(hipError_t e, const char* what) {
+    err = std::string(what) + ": " + hipGetErrorString(e);
+    return e == hipErrorOutOfMemory ? BH_ERR_OOM : BH_ERR_HIP;
+}
+
+bool bh_ctx::injected(int op, int* status) {
+    if (inj_count <= 0) return false;
+    if (inj_op != BH_OP_ANY && inj_op != op) return false;
+    --inj_count;
+    *status = inj_status;
+    err = "injected fault (op " + std::to_string(op) + ")";
+    return true;
+}
+
+int bh_ctx::ensure_scratch(size_t xb, size_t yb) {
+    if (xb > x_cap) {
+        if (d_x) hipFree(d_x);
+        d_x = nullptr;
+        x_cap = 0;
+        hipError_t e = hipMalloc(&d_x, xb);
+        if (e != hipSuccess) return hip_fail(e, "hipMalloc(scratch x)");
+        x_cap = xb;
+    }
+    if (yb > y_cap) {
+        if (d_y) hipFree(d_y);
+        d_y = nullptr;
+        y_cap = 0;
+        hipError_t e = hipMalloc(&d_y, yb);
+        if (e != hipSuccess) return hip_fail(e, "hipMalloc(scratch y)");
+        y_cap = yb;
+    }
+    return BH_OK;
+}
+
+namespace bh {
+
+void free_weight(DevWeight& w) {
+    if (w.q) hipFree(w.q);
+    if (w.s) hipFree(w.s);
+    w = DevWeight();
+}
+
+// Allocate a KM16 device weight of n rows (padded) and zero it.
+int alloc_weight(bh_ctx* ctx, int fmt, int64_t n, int64_t k, DevWeight& w) {
+    const int E = chunk_elems(fmt);
+    if (n <= 0 || k <= 0 || k % E != 0)
+        return ctx->fail(BH_ERR_UNSUPPORTED, "weight " + std::to_string(n) + "x" + std::to_string(k) +
+                                                 ": in_features must be a positive multiple of " + std::to_string(E));
+    w.fmt = fmt;
+    w.n = n;
+    w.k = k;
+    w.n_pad = pad64(n);
+    w.chunks = k / E;
+    const size_t qb = (size_t)(w.chunks * w.n_pad * 16);
+    size_t sb = 0;
+    if (fmt == BH_Q4_G32) sb = (size_t)(w.chunks * w.n_pad * 2);
+    if (fmt == BH_Q8_ROW || fmt == BH_Q4_ROW) sb = (size_t)w.n_pad * 4;
+    hipError_t e = hipMalloc(&w.q, qb);
+    if (e != hipSuccess) {
+        w.q = nullptr;
+        return ctx->hip_fail(e, "hipMalloc(weight)");
+    }
+    e = hipMemset(w.q, 0, qb);
+    if (e != hipSuccess) return ctx->hip_fail(e, "hipMemset(weight)");
+    if (sb) {
+        e = hipMalloc(&w.s, sb);
+        if (e != hipSuccess) {
+            w.s = nullptr;
+            free_weight(w);
+            return ctx->hip_fail(e, "hipMalloc(scales)");
+        }
+        e = hipMemset(w.s, 0, sb);
+        if (e != hipSuccess) return ctx->hip_fail(e, "hipMemset(scales)");
+    }
+    w.bytes = qb + sb;
+    return BH_OK;
+}
+
+// Expected host byte counts of a reference-layout weight.
+bool host_sizes(int fmt, int64_t n, int64_t k, size_t* qb, size_t* sb) {
+    switch (fmt) {
+        case BH_F32: *qb = (size_t)(n * k * 4); *sb = 0; return true;
+        case BH_Q8_ROW: *qb = (size_t)(n * k); *sb = (size_t)n * 4; return true;
+        case BH_Q4_ROW: *qb = (size_t)(n * (k / 2)); *sb = (size_t)n * 4; return true;
+        case BH_Q4_G32: *qb = (size_t)(n * (k / 2)); *sb = (size_t)(n * (k / 32)) * 2; return true;
+        default: return false;
+    }
+}
+
+// Write rows [row0, row0 + n) of `dst` from a reference-layout host weight.
+int upload_rows(bh_ctx* ctx, DevWeight& dst, int64_t row0, int64_t n, const void* q, size_t q_bytes, const void* s,
+                size_t s_bytes) {
+    size_t eq, es;
+    if (!host_sizes(dst.fmt, n, dst.k, &eq, &es)) return ctx->fail(BH_ERR_INVALID, "unknown weight format");
+    if (q_bytes != eq || (es && s_bytes != es) || !q || (es && !s))
+        return ctx->fail(BH_ERR_INVALID, "weight size mismatch: got " + std::to_string(q_bytes) + "/" +
+                                             std::to_string(s_bytes) + " bytes, expected " + std::to_string(eq) +
+                                             "/" + std::to_string(es) + " for " + std::to_string(n) + "x" +
+                                             std::to_string(dst.k));
+    if (row0 < 0 || row0 + n > dst.n) return ctx->fail(BH_ERR_INVALID, "row range outside the weight");
+    std::string err;
+    void *hq = nullptr, *hs = nullptr;
+    size_t hqb = 0, hsb = 0;
+    if (!repack_km16(dst.fmt, n, dst.k, q, s, err, &hq, &hqb, &hs, &hsb)) return ctx->fail(BH_ERR_UNSUPPORTED, err);
+    const int64_t np_src = pad64(n);
+    hipError_t e = hipMemcpy2D((uint8_t*)dst.q + row0 * 16, (size_t)dst.n_pad * 16, hq, (size_t)np_src * 16,
+                               (size_t)n * 16, (size_t)dst.chunks, hipMemcpyHostToDevice);
+    if (e == hipSuccess && dst.fmt == BH_Q4_G32)
+        e = hipMemcpy2D((uint8_t*)dst.s + row0 * 2, (size_t)dst.n_pad * 2, hs, (size_t)np_src * 2, (size_t)n * 2,
+                        (size_t)dst.chunks, hipMemcpyHostToDevice);
+    else if (e == hipSuccess && (dst.fmt == BH_Q8_ROW || dst.fmt == BH_Q4_ROW))
+        e = hipMemcpy((float*)dst.s + row0, hs, (size_t)n * 4, hipMemcpyHostToDevice);
+    free(hq);
+    free(hs);
+    if (e != hipSuccess) return ctx->hip_fail(e, "hipMemcpy(weight)");
+    return BH_OK;
+}
+
+}  // namespace bh
+
+// --------------------------------------------------------------- registry
+void bh_ctx::touch(const std::string& key) {
+    auto it = reg.find(key);
+    if (it == reg.end()) return;
+    lru.erase(it->second.lru_it);
+    lru.push_back(key);
+    it->second.lru_it = std::prev(lru.end());
+}
+
+// ModelBuffers::enforce_limits (wgpu_backend.rs:67-81): evict least recently used
+// entries until the new bytes fit under the cap.
+void bh_ctx::enforce_limits(size_t new_bytes) {
+    while (used + new_bytes > cap && !lru.empty()) {
+        const std::string key = lru.front();
+        lru.pop_front();
+        auto it = reg.find(key);
+        if (it != reg.end()) {
+            used -= std::min(used, it->second.w.bytes);
+            free_weight(it->second.w);
+            reg.erase(it);
+        }
+    }
+}
+
+void bh_ctx::clear_registry() {
+    for (auto& kv : reg) free_weight(kv.second.w);
+    reg.clear();
+    lru.clear();
+    used = 0;
+}
+
+// The shared body of the three matvec mirrors.
+static int matvec_common(bh_ctx* ctx, int fmt, const float* h, size_t in_f, const void* q, size_t q_len,
+                         size_t q_expect, const float* scales, size_t s_len, size_t out_f, const char* model,
+                         const char* layer, float* out) {
+    if (!ctx) return BH_ERR_INVALID;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    int st;
+    if (ctx->injected(BH_OP_MATVEC, &st)) return st;
+    if (out_f > 0 && !out) return ctx->fail(BH_ERR_INVALID, "out is NULL");
+    if (in_f == 0 || out_f == 0) {  // wgpu_backend.rs:1093-1095
+        if (out_f) std::memset(out, 0, out_f * 4);
+        return BH_OK;
+    }
+    if (!h || !q) return ctx->fail(BH_ERR_INVALID, "input is NULL");
+    const char* what = fmt == BH_F32 ? "Weight" : (fmt == BH_Q8_ROW ? "Quantized INT8 weight" : "Quantized INT4 weight");
+    if (q_len != q_expect)  // wgpu_backend.rs:1096-1104
+        return ctx->fail(BH_ERR_INVALID, std::string(what) + " size mismatch: weight length is " +
+                                             std::to_string(q_len) + ", expected " + std::to_string(q_expect));
+    if (fmt != BH_F32 && (!scales || s_len != out_f))
+        return ctx->fail(BH_ERR_INVALID, "scales length is " + std::to_string(s_len) + ", expected " +
+                                             std::to_string(out_f));
+    const int64_t k = fmt == BH_Q4_ROW ? (int64_t)(in_f / 2) * 2 : (int64_t)in_f;
+    if (fmt == BH_Q4_ROW && (in_f % 2))
+        return ctx->fail(BH_ERR_UNSUPPORTED, "INT4 GEMV needs an even in_features");
+
+    DevWeight tmp;
+    const DevWeight* w = nullptr;
+    std::string key;
+    const bool keyed = model && layer;
+    if (keyed) {
+        key = std::string(model) + ":" + layer;
+        auto it = ctx->reg.find(key);
+        if (it != ctx->reg.end()) {
+            const DevWeight& cw = it->second.w;
+            if (cw.fmt != fmt || cw.n != (int64_t)out_f || cw.k != k)
+                return ctx->fail(BH_ERR_INVALID, "registry entry '" + key + "' holds a " + std::to_string(cw.n) +
+                                                     "x" + std::to_string(cw.k) + " weight of another format/shape");
+            ctx->touch(key);
+            w = &cw;
+        }
+    }
+    if (!w) {
+        int rc = alloc_weight(ctx, fmt, (int64_t)out_f, k, tmp);
+        if (rc) return rc;
+        rc = upload_rows(ctx, tmp, 0, (int64_t)out_f, q, q_len * (fmt == BH_F32 ? 4 : 1), scales,
+                         fmt == BH_F32 ? 0 : out_f * 4);
+        if (rc) {
+            free_weight(tmp);
+            return rc;
+        }
+        if (keyed) {
+            ctx->enforce_limits(tmp.bytes);
+            auto& ent = ctx->reg[key];
+            ent.w = tmp;
+            ctx->lru.push_back(key);
+            ent.lru_it = std::prev(ctx->lru.end());
+            ctx->used += tmp.bytes;
+            tmp = DevWeight();
+            w = &ent.w;
+        } else {
+            w = &tmp;
+        }
+    }
+    int rc = ctx->ensure_scratch(in_f * 4, out_f * 4);
+    if (rc) {
+        free_weight(tmp);
+        return rc;
+    }
+    hipError_t e = hipMemcpyAsync(ctx->d_x, h, in_f * 4, hipMemcpyHostToDevice, ctx->stream);
+    GemvArgs a;
+    a.W = w->q;
+    a.S = w->s;
+    a.x = (const float*)ctx->d_x;
+    a.ldx = (int64_t)in_f;
+    a.y = (float*)ctx->d_y;
+    a.ldy = (int64_t)out_f;
+    a.N = (int)w->n;
+    a.n_pad = (int)w->n_pad;
+    a.C = (int)w->chunks;
+    a.batch = 1;
+    if (e == hipSuccess) e = launch_gemv(fmt, EPI_STORE, a, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(out, ctx->d_y, out_f * 4, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    free_weight(tmp);
+    if (e != hipSuccess) return ctx->hip_fail(e, "matvec");
+    return BH_OK;
+}
+
+extern "C" {
+
+const char* bh_status_str(int s) {
+    switch (s) {
+        case BH_OK: return "ok";
+        case BH_ERR_INVALID: return "invalid argument";
+        case BH_ERR_NO_DEVICE: return "no usable gfx950 device";
+        case BH_ERR_HIP: return "HIP runtime error";
+        case BH_ERR_OOM: return "device out of memory";
+        case BH_ERR_NOT_FOUND: return "not found";
+        case BH_ERR_INJECTED: return "injected fault";
+        case BH_ERR_UNSUPPORTED: return "unsupported shape or format";
+        case BH_ERR_CAPACITY: return "capacity exceeded";
+        default: return "unknown status";
+    }
+}
+
+int bh_init(int device, bh_ctx** out) {
+    if (!out) return BH_ERR_INVALID;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0 || device < 0 || device >= n) return BH_ERR_NO_DEVICE;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) return BH_ERR_NO_DEVICE;
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return BH_ERR_NO_DEVICE;
+    if (hipSetDevice(device) != hipSuccess) return BH_ERR_NO_DEVICE;
+    bh_ctx* c = new bh_ctx();
+    c->device = device;
+    c->n_cu = prop.multiProcessorCount;
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return BH_ERR_HIP;
+    }
+    *out = c;
+    return BH_OK;
+}
+
+void bh_destroy(bh_ctx* ctx) {
+    if (!ctx) return;
+    hipSetDevice(ctx->device);
+    hipStreamSynchronize(ctx->stream);
+    ctx->clear_registry();
+    if (ctx->d_x) hipFree(ctx->d_x);
+    if (ctx->d_y) hipFree(ctx->d_y);
+    for (auto& kv : ctx->rope_tabs) hipFree(kv.second);
+    if (ctx->attn_part) hipFree(ctx->attn_part);
+    hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+const char* bh_last_error(const bh_ctx* ctx) { return ctx ? ctx->err.c_str() : "no context"; }
+
+int bh_set_vram_cap(bh_ctx* ctx, size_t bytes) {
+    if (!ctx) return BH_ERR_INVALID;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    ctx->cap = bytes;
+    ctx->enforce_limits(0);
+    return BH_OK;
+}
+
+int bh_registry_stats(bh_ctx* ctx, size_t* n_entries, size_t* bytes) {
+    if (!ctx) return BH_ERR_INVALID;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (n_entries) *n_entries = ctx->reg.size();
+    if (bytes) *bytes = ctx->used;
+    return BH_OK;
+}
+
+int bh_debug_inject_fault(bh_ctx* ctx, int op, int status, int count) {
+    if (!ctx) return BH_ERR_INVALID;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    ctx->inj_op = op;
+    ctx->inj_status = status == 0 ? BH_ERR_INJECTED : status;
+    ctx->inj_count = count;
+    return BH_OK;
+}
+
+int bh_matvec_mul(bh_ctx* ctx, const float* h, size_t in_features, const float* weight, size_t weight_len,
+                  size_t out_features, const char* model_name, const char* layer_name, float* out) {
+    return matvec_common(ctx, BH_F32, h, in_features, weight, weight_len, out_features * in_features, nullptr, 0,
+                         out_features, model_name, layer_name, out);
+}
+
+int bh_matvec_mul_int8(bh_ctx* ctx, const float* h, size_t in_features, const int8_t* q_weight, size_t q_len,
+                       const float* scales, size_t s_len, size_t out_features, const char* model_name,
+                       const char* layer_name, float* out) {
+    return matvec_common(ctx, BH_Q8_ROW, h, in_features, q_weight, q_len, out_features * in_features, scales, s_len,
+                         out_features, model_name, layer_name, out);
+}
+
+int bh_matvec_mul_int4(bh_ctx* ctx, const float* h, size_t in_features, const uint8_t* q_weight, size_t q_len,
+                       const float* scales, size_t s_len, size_t out_features, const char* model_name,
+                       const char* layer_name, float* out) {
+    return matvec_common(ctx, BH_Q4_ROW, h, in_features, q_weight, q_len, out_features * (in_features / 2), scales,
+                         s_len, out_features, model_name, layer_name, out);
+}
+
+int bh_clear_persistent_buffers(bh_ctx* ctx) {
+    if (!ctx) return BH_ERR_INVALID;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    hipStreamSynchronize(ctx->stream);
+    ctx->clear_registry();
+    return BH_OK;
+}
+
+// ------------------------------------------------------ device-resident weights
+int bh_weight_upload(bh_ctx* ctx, int fmt, int64_t n_out, int64_t k_in, const void* q, size_t q_bytes,
+                     const void* scales, size_t s_bytes, bh_weight** out) {
+    if (!ctx || !out) return BH_ERR_INVALID;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    int st;
+    if (ctx->injected(BH_OP_UPLOAD, &st)) return st;
+    if (fmt < BH_F32 || fmt > BH_Q4_G32) return ctx->fail(BH_ERR_INVALID, "unknown format");
+    DevWeight w;
+    int rc = alloc_weight(ctx, fmt, n_out, k_in, w);
+    if (rc) return rc;
+    rc = upload_rows(ctx, w, 0, n_out, q, q_bytes, scales, s_bytes);
+    if (rc) {
+        free_weight(w);
+        return rc;
+    }
+    *out = (bh_weight*)new DevWeight(w);
+    return BH_OK;
+}
+
+void bh_weight_free(bh_ctx* ctx, bh_weight* w) {
+    if (!w) return;
+    if (ctx) hipStreamSynchronize(ctx->stream);
+    DevWeight* d = (DevWeight*)w;
+    free_weight(*d);
+    delete d;
+}
+
+static hipStream_t pick(bh_ctx* ctx, void* stream) { return stream ? (hipStream_t)stream : ctx->stream; }
+
+int bh_gemv(bh_ctx* ctx, const bh_weight* wh, const float* x, float* y, int batch, void* stream) {
+    if (!ctx || !wh || !x || !y || batch < 0) return BH_ERR_INVALID;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    int st;
+    if (ctx->injected(BH_OP_GEMV, &st)) return st;
+    if (batch == 0) return BH_OK;
+    const DevWeight* w = (const DevWeight*)wh;
+    GemvArgs a;
+    a.W = w->q;
+    a.S = w->s;
+    a.x = x;
+    a.ldx = w->k;
+    a.y = y;
+    a.ldy = w->n;
+    a.N = (int)w->n;
+    a.n_pad = (int)w->n_pad;
+    a.C = (int)w->chunks;
+    a.batch = batch;
+    hipError_t e = launch_gemv(w->fmt, EPI_STORE, a, pick(ctx, stream));
+    return e == hipSuccess ? BH_OK : ctx->hip_fail(e, "gemv launch");
+}
+
+int bh_dequant(bh_ctx* ctx, const bh_weight* wh, float* out, void* stream) {
+    if (!ctx || !wh || !out) return BH_ERR_INVALID;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    hipError_t e = launch_dequant(*(const DevWeight*)wh, out, pick(ctx, stream));
+    return e == hipSuccess ? BH_OK : ctx->hip_fail(e, "dequant launch");
+}
+
+// ------------------------------------------------------------ single ops
+int bh_rmsnorm(bh_ctx* ctx, const float* x, const float* w, float eps, float* out, int rows, int n, void* stream) {
+    if (!ctx || !x || !w || !out || rows < 0 || n <= 0) return BH_ERR_INVALID;
+    if (rows == 0) return BH_OK;
+    hipError_t e = launch_rmsnorm(x, w, eps, out, rows, n, pick(ctx, stream));
+    return e == hipSuccess ? BH_OK : ctx->hip_fail(e, "rmsnorm launch");
+}
+
+const float2* bh_ctx::rope_tab(int hd, float theta, int max_pos) {
+    char key[96];
+    std::snprintf(key, sizeof key, "%d:%08x:%d", hd, *(const uint32_t*)&theta, max_pos);
+    auto it = rope_tabs.find(key);
+    if (it != rope_tabs.end()) return (const float2*)it->second;
+    std::vector<float2> h((size_t)max_pos * (hd / 2));
+    rope_table(hd, theta, max_pos, h.data());
+    void* d = nullptr;
+    if (hipMalloc(&d, h.size() * sizeof(float2)) != hipSuccess) return nullptr;
+    if (hipMemcpy(d, h.data(), h.size() * sizeof(float2), hipMemcpyHostToDevice) != hipSuccess) {
+        hipFree(d);
+        return nullptr;
+    }
+    rope_tabs[key] = d;
+    return (const float2*)d;
+}
+
+int bh_rope(bh_ctx* ctx, float* v, const int32_t* pos, int rows, int n_heads, int head_dim, float theta, int max_pos,
+            void* stream) {
+    if (!ctx || !v || !pos || rows < 0 || n_heads <= 0 || head_dim <= 0 || head_dim % 2 || max_pos <= 0)
+        return BH_ERR_INVALID;
+    if (rows == 0) return BH_OK;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    const float2* tab = ctx->rope_tab(head_dim, theta, max_pos);
+    if (!tab) return ctx->fail(BH_ERR_OOM, "rope table");
+    hipError_t e = launch_rope(v, pos, tab, rows, n_heads, head_dim, pick(ctx, stream));
+    return e == hipSuccess ? BH_OK : ctx->hip_fail(e, "rope launch");
+}
+
+int bh_silu_mul(bh_ctx* ctx, const float* g, const float* u, float* out, int64_t n, void* stream) {
+    if (!ctx || !g || !u || !out || n < 0) return BH_ERR_INVALID;
+    if (n == 0) return BH_OK;
+    hipError_t e = launch_silu_mul(g, u, out, n, pick(ctx, stream));
+    return e == hipSuccess ? BH_OK : ctx->hip_fail(e, "silu launch");
+}
+
+int bh_attn_decode(bh_ctx* ctx, const float* q, const void* k, const void* v, int kv_f16, int64_t kv_rows,
+                   const int64_t* seq_off, const int32_t* seq_len, int batch, int n_q, int n_kv, int head_dim,
+                   int max_len, float* out, void* stream) {
+    if (!ctx || !q || !k || !v || !seq_off || !seq_len || !out || batch < 0 || n_q <= 0 || n_kv <= 0 ||
+        n_q % n_kv || max_len < 0)
+        return BH_ERR_INVALID;
+    if (head_dim != 64 && head_dim != 128)
+        return ctx->fail(BH_ERR_UNSUPPORTED, "attention supports head_dim 64 and 128");
+    if (n_q / n_kv > 8) return ctx->fail(BH_ERR_UNSUPPORTED, "attention supports up to 8 query heads per KV head");
+    if (batch == 0) return BH_OK;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    AttnArgs a;
+    a.q = q;
+    a.out = out;
+    a.kv.k = (void*)k;
+    a.kv.v = (void*)v;
+    a.kv.kv_rows = kv_rows;
+    a.kv.kv_f16 = kv_f16 ? 1 : 0;
+    a.seq_off = seq_off;
+    a.seq_len = seq_len;
+    a.batch = batch;
+    a.nq = n_q;
+    a.nkv = n_kv;
+    a.hd = head_dim;
+    attn_plan(std::max(max_len, 1), batch, n_kv, &a.splits, &a.split_rows);
+    if (a.splits > 1) {
+        const size_t need = (size_t)batch * n_q * a.splits * (head_dim + 2) * 4;
+        if (need > ctx->attn_part_bytes) {
+            if (ctx->attn_part) hipFree(ctx->attn_part);
+            ctx->attn_part = nullptr;
+            ctx->attn_part_bytes = 0;
+            hipError_t e = hipMalloc(&ctx->attn_part, need);
+            if (e != hipSuccess) return ctx->hip_fail(e, "hipMalloc(attention partials)");
+            ctx->attn_part_bytes = need;
+        }
+        a.part_o = (float*)ctx->attn_part;
+        a.part_ml = a.part_o + (size_t)batch * n_q * a.splits * head_dim;
+    }
+    hipError_t e = launch_attention(a, pick(ctx, stream));
+    return e == hipSuccess ? BH_OK : ctx->hip_fail(e, "attention launch");
+}
+
+}  // extern "C"

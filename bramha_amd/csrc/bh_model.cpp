@@ -1,0 +1,791 @@
+// bh_model.cpp — the dense Qwen2/Llama decoder on the device: weights, the packed
+// KV cache, prefill, and graph-replayed greedy decode steps.
+//
+// Reference: generate_cpu_inner_logits (src/inference/cpu_engine.rs:2290-3064) with
+// CPU-only mode and temperature 0. One forward pass over M tokens is
+//   embed -> L x [rmsnorm, QKV(+bias, RoPE, KV append), attention, O(+bias)+residual,
+//                 rmsnorm, gate/up + SiLU gate, down + residual]
+//         -> [final rmsnorm, LM head + repetition penalty + argmax]   (decode only)
+// Sequences own consecutive regions of one packed KV buffer per layer (offsets are
+// prefix sums of the regions' capacities); a decode step reads its token from the
+// previous step's argmax and its position from the sequence's row count, both on the
+// device, so the whole step is captured once as a HIP graph and replayed.
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+#include "bh_ctx.h"
+
+using namespace bh;
+
+namespace {
+
+enum Tensor { T_LN1, T_LN2, T_Q, T_K, T_V, T_O, T_GATE, T_UP, T_DOWN, T_BQ, T_BK, T_BV, T_BO, T_COUNT };
+
+struct LayerW {
+    DevWeight qkv, o, gate, up, down;
+    float* ln1 = nullptr;
+    float* ln2 = nullptr;
+    float* bqkv = nullptr;
+    float* bo = nullptr;
+    uint32_t have = 0;
+};
+
+struct TimerRec {
+    int cls;
+    hipEvent_t a, b;
+};
+
+}  // namespace
+
+struct bh_model {
+    bh_ctx* ctx = nullptr;
+    bh_model_config c{};
+    hipStream_t st = nullptr;
+    int64_t QD = 0, KD = 0, NQKV = 0;
+    int tiles_lm = 0;
+    std::vector<LayerW> L;
+    DevWeight embed;
+    bool have_embed = false;
+    float* norm = nullptr;
+    bool have_norm = false;
+
+    std::vector<void*> kc, vc;
+    float *x = nullptr, *h = nullptr, *q = nullptr, *att = nullptr, *mm = nullptr, *logits = nullptr;
+    float* part_val = nullptr;
+    int32_t* part_idx = nullptr;
+    float* attn_part = nullptr;
+    int max_splits = 128;
+    // decode batch inputs (read by the captured graph) and prefill inputs, kept apart so a
+    // prefill between decode calls leaves the batch intact
+    int32_t *d_tok = nullptr, *d_pos = nullptr, *d_slot = nullptr;
+    int32_t *d_ptok = nullptr, *d_ppos = nullptr, *d_pslot = nullptr;
+    int32_t *d_seq_len = nullptr, *d_step = nullptr;
+    int64_t* d_seq_off = nullptr;
+    uint32_t *d_next = nullptr, *d_ids = nullptr;
+    int64_t ids_steps = 1024;
+    uint16_t* d_pen = nullptr;
+    const float2* rope = nullptr;
+    int max_pos = 0;
+    int32_t* h_stage = nullptr;  // pinned: [3 * max_tokens + 2]
+
+    std::vector<int64_t> off_h, cap_h;
+    std::vector<int32_t> len_h;
+    std::vector<char> open_h;
+    int64_t next_free = 0;
+
+    int B = 0;
+    std::vector<int32_t> bslots;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t gexec = nullptr;
+    int g_B = 0, g_splits = 0, g_rows = 0;
+
+    bool timing = false;
+    std::vector<TimerRec> recs;
+    std::vector<hipEvent_t> ev_pool;
+    size_t ev_used = 0;
+
+    std::vector<void*> allocs;  // device buffers owned by the model
+
+    int fail(int s, const std::string& m) { return ctx->fail(s, m); }
+};
+
+namespace {
+
+hipError_t dmalloc(bh_model* m, void** p, size_t bytes) {
+    *p = nullptr;
+    hipError_t e = hipMalloc(p, std::max<size_t>(bytes, 16));
+    if (e == hipSuccess) {
+        m->allocs.push_back(*p);
+        e = hipMemset(*p, 0, std::max<size_t>(bytes, 16));
+    }
+    return e;
+}
+
+hipEvent_t next_event(bh_model* m) {
+    if (m->ev_used == m->ev_pool.size()) {
+        hipEvent_t e;
+        hipEventCreate(&e);
+        m->ev_pool.push_back(e);
+    }
+    return m->ev_pool[m->ev_used++];
+}
+
+template <class F>
+hipError_t timed(bh_model* m, int cls, F&& f) {
+    if (!m->timing) return f();
+    hipEvent_t a = next_event(m), b = next_event(m);
+    hipEventRecord(a, m->st);
+    hipError_t e = f();
+    hipEventRecord(b, m->st);
+    m->recs.push_back({cls, a, b});
+    return e;
+}
+
+KvView kv_view(bh_model* m, int l) {
+    KvView v;
+    v.k = m->kc[l];
+    v.v = m->vc[l];
+    v.kv_rows = m->c.kv_rows;
+    v.kv_f16 = m->c.kv_f16;
+    v.max_context = m->c.max_context > 0 ? m->c.max_context : 0;
+    v.sink = m->c.sink_tokens;
+    return v;
+}
+
+// One forward pass over M tokens: the decode batch (decode = true: tokens from the last
+// argmax, positions from the row counts, logits and sampling) or a staged prefill chunk.
+hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) {
+    const bh_model_config& c = m->c;
+    const int H = c.hidden, I = c.ffn;
+    hipStream_t st = m->st;
+    int32_t* tok = decode ? m->d_tok : m->d_ptok;
+    int32_t* pos = decode ? m->d_pos : m->d_ppos;
+    int32_t* slot = decode ? m->d_slot : m->d_pslot;
+    const bool logits = decode;
+    hipError_t e = timed(m, BH_K_OTHER, [&] {
+        return launch_embed(m->embed, tok, pos, slot, m->d_seq_len, m->d_next, decode ? 1 : 0, m->x, H, M, st);
+    });
+    for (int l = 0; l < c.n_layers && e == hipSuccess; ++l) {
+        LayerW& w = m->L[l];
+        e = timed(m, BH_K_NORM, [&] { return launch_rmsnorm(m->x, w.ln1, c.rms_eps, m->h, M, H, st); });
+        if (e != hipSuccess) break;
+        GemvArgs a;
+        a.W = w.qkv.q;
+        a.S = w.qkv.s;
+        a.x = m->h;
+        a.ldx = H;
+        a.y = m->q;
+        a.ldy = m->QD;
+        a.bias = c.attn_bias ? w.bqkv : nullptr;
+        a.N = (int)m->NQKV;
+        a.n_pad = (int)w.qkv.n_pad;
+        a.C = (int)w.qkv.chunks;
+        a.batch = M;
+        a.qd = (int)m->QD;
+        a.kd = (int)m->KD;
+        a.hd = c.head_dim;
+        a.pos = pos;
+        a.slot = slot;
+        a.seq_off = m->d_seq_off;
+        a.rope = m->rope;
+        a.kv = kv_view(m, l);
+        e = timed(m, BH_K_GEMV_QKV, [&] { return launch_gemv(c.wfmt, EPI_QKV, a, st); });
+        if (e != hipSuccess) break;
+        AttnArgs at;
+        at.q = m->q;
+        at.out = m->att;
+        at.kv = kv_view(m, l);
+        at.pos = pos;
+        at.slot = slot;
+        at.seq_off = m->d_seq_off;
+        at.batch = M;
+        at.nq = c.n_heads;
+        at.nkv = c.n_kv_heads;
+        at.hd = c.head_dim;
+        at.splits = splits;
+        at.split_rows = split_rows;
+        at.part_o = m->attn_part;
+        at.part_ml = m->attn_part + (size_t)c.max_tokens * c.n_heads * m->max_splits * c.head_dim;
+        e = timed(m, BH_K_ATTN, [&] { return launch_attention(at, st); });
+        if (e != hipSuccess) break;
+        GemvArgs o;
+        o.W = w.o.q;
+        o.S = w.o.s;
+        o.x = m->att;
+        o.ldx = m->QD;
+        o.y = m->x;
+        o.ldy = H;
+        o.bias = c.o_bias ? w.bo : nullptr;
+        o.N = H;
+        o.n_pad = (int)w.o.n_pad;
+        o.C = (int)w.o.chunks;
+        o.batch = M;
+        e = timed(m, BH_K_GEMV_O, [&] { return launch_gemv(c.wfmt, EPI_RESID, o, st); });
+        if (e != hipSuccess) break;
+        e = timed(m, BH_K_NORM, [&] { return launch_rmsnorm(m->x, w.ln2, c.rms_eps, m->h, M, H, st); });
+        if (e != hipSuccess) break;
+        GemvArgs gu;
+        gu.W = w.gate.q;
+        gu.S = w.gate.s;
+        gu.W2 = w.up.q;
+        gu.S2 = w.up.s;
+        gu.x = m->h;
+        gu.ldx = H;
+        gu.y = m->mm;
+        gu.ldy = I;
+        gu.N = I;
+        gu.n_pad = (int)w.gate.n_pad;
+        gu.C = (int)w.gate.chunks;
+        gu.batch = M;
+        e = timed(m, BH_K_GEMV_GATEUP, [&] { return launch_gemv(c.wfmt, EPI_SILU, gu, st); });
+        if (e != hipSuccess) break;
+        GemvArgs d;
+        d.W = w.down.q;
+        d.S = w.down.s;
+        d.x = m->mm;
+        d.ldx = I;
+        d.y = m->x;
+        d.ldy = H;
+        d.N = H;
+        d.n_pad = (int)w.down.n_pad;
+        d.C = (int)w.down.chunks;
+        d.batch = M;
+        e = timed(m, BH_K_GEMV_DOWN, [&] { return launch_gemv(c.wfmt, EPI_RESID, d, st); });
+    }
+    if (e != hipSuccess || !logits) return e;
+    e = timed(m, BH_K_NORM, [&] { return launch_rmsnorm(m->x, m->norm, c.rms_eps, m->h, M, H, st); });
+    if (e != hipSuccess) return e;
+    GemvArgs lm;
+    lm.W = m->embed.q;
+    lm.S = m->embed.s;
+    lm.x = m->h;
+    lm.ldx = H;
+    lm.y = m->logits;
+    lm.ldy = c.vocab;
+    lm.N = c.vocab;
+    lm.n_pad = (int)m->embed.n_pad;
+    lm.C = (int)m->embed.chunks;
+    lm.batch = M;
+    lm.pen = m->d_pen;
+    lm.vocab = c.vocab;
+    lm.slot = slot;
+    lm.part_val = m->part_val;
+    lm.part_idx = m->part_idx;
+    e = timed(m, BH_K_LM_HEAD, [&] { return launch_gemv(c.head_fmt, EPI_LMHEAD, lm, st); });
+    if (e != hipSuccess) return e;
+    e = timed(m, BH_K_OTHER, [&] {
+        hipError_t r = launch_sample_final(m->part_val, m->part_idx, m->tiles_lm, M, slot, m->d_pen, c.vocab,
+                                           m->d_next, m->d_ids, m->d_step, st);
+        if (r == hipSuccess) r = launch_step_counter(m->d_step, 0, st);
+        return r;
+    });
+    return e;
+}
+
+int64_t layer_tensor_count(const bh_model_config& c) { return 9 + (c.attn_bias ? 3 : 0) + (c.o_bias ? 1 : 0); }
+
+bool parse_layer(const char* name, int* l, const char** rest) {
+    if (std::strncmp(name, "model.layers.", 13) != 0) return false;
+    const char* p = name + 13;
+    if (*p < '0' || *p > '9') return false;
+    int v = 0;
+    while (*p >= '0' && *p <= '9') v = v * 10 + (*p++ - '0');
+    if (*p != '.') return false;
+    *l = v;
+    *rest = p + 1;
+    return true;
+}
+
+int set_vec(bh_model* m, float** dst, int64_t n, const void* data, size_t bytes, const char* name) {
+    if (bytes != (size_t)n * 4 || !data)
+        return m->fail(BH_ERR_INVALID, std::string(name) + ": expected " + std::to_string(n * 4) + " bytes, got " +
+                                           std::to_string(bytes));
+    if (!*dst) {
+        hipError_t e = dmalloc(m, (void**)dst, (size_t)n * 4);
+        if (e != hipSuccess) return m->ctx->hip_fail(e, "hipMalloc(vector)");
+    }
+    hipError_t e = hipMemcpy(*dst, data, (size_t)n * 4, hipMemcpyHostToDevice);
+    return e == hipSuccess ? BH_OK : m->ctx->hip_fail(e, "hipMemcpy(vector)");
+}
+
+int set_bias_part(bh_model* m, LayerW& w, int64_t off, int64_t n, const void* data, size_t bytes, const char* name) {
+    if (bytes != (size_t)n * 4 || !data)
+        return m->fail(BH_ERR_INVALID, std::string(name) + ": expected " + std::to_string(n * 4) + " bytes");
+    if (!w.bqkv) {
+        hipError_t e = dmalloc(m, (void**)&w.bqkv, (size_t)m->NQKV * 4);
+        if (e != hipSuccess) return m->ctx->hip_fail(e, "hipMalloc(bias)");
+    }
+    hipError_t e = hipMemcpy(w.bqkv + off, data, (size_t)n * 4, hipMemcpyHostToDevice);
+    return e == hipSuccess ? BH_OK : m->ctx->hip_fail(e, "hipMemcpy(bias)");
+}
+
+int ensure_weight(bh_model* m, DevWeight& w, int fmt, int64_t n, int64_t k) {
+    if (w.q) return BH_OK;
+    return alloc_weight(m->ctx, fmt, n, k, w);
+}
+
+void drop_graph(bh_model* m) {
+    if (m->gexec) hipGraphExecDestroy(m->gexec);
+    if (m->graph) hipGraphDestroy(m->graph);
+    m->gexec = nullptr;
+    m->graph = nullptr;
+    m->g_B = m->g_splits = m->g_rows = 0;
+}
+
+// Largest attention length the next n_steps decode steps of the batch can reach.
+int decode_len_bound(bh_model* m, int n_steps) {
+    int64_t mx = 1;
+    for (int b = 0; b < m->B; ++b) {
+        const int s = m->bslots[b];
+        int64_t len = m->len_h[s] + n_steps;
+        if (m->c.max_context > 0) len = std::min<int64_t>(len, m->c.max_context);
+        mx = std::max(mx, len);
+    }
+    return (int)mx;
+}
+
+int check_decode_room(bh_model* m, int n_steps) {
+    for (int b = 0; b < m->B; ++b) {
+        const int s = m->bslots[b];
+        if (!m->open_h[s]) return m->fail(BH_ERR_INVALID, "decode batch holds a slot that is not open");
+        const int64_t end = m->len_h[s] + n_steps;
+        if (end > m->max_pos) return m->fail(BH_ERR_CAPACITY, "position beyond the RoPE table");
+        if (m->c.max_context <= 0 && end > m->cap_h[s])
+            return m->fail(BH_ERR_CAPACITY, "slot " + std::to_string(s) + " needs " + std::to_string(end) +
+                                                " KV rows, has " + std::to_string(m->cap_h[s]));
+    }
+    return BH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int bh_model_create(bh_ctx* ctx, const bh_model_config* cfg, bh_model** out) {
+    if (!ctx || !cfg || !out) return BH_ERR_INVALID;
+    *out = nullptr;
+    const bh_model_config& c = *cfg;
+    if (c.n_layers <= 0 || c.hidden <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.ffn <= 0 || c.vocab <= 0 ||
+        c.n_heads % c.n_kv_heads || c.max_seqs <= 0 || c.kv_rows <= 0 || c.max_tokens <= 0)
+        return ctx->fail(BH_ERR_INVALID, "invalid model config");
+    if (c.head_dim != 64 && c.head_dim != 128)
+        return ctx->fail(BH_ERR_UNSUPPORTED, "head_dim must be 64 or 128");
+    if (c.n_heads / c.n_kv_heads > 8) return ctx->fail(BH_ERR_UNSUPPORTED, "at most 8 query heads per KV head");
+    if (c.head_fmt != BH_F32 && c.head_fmt != BH_Q4_G32)
+        return ctx->fail(BH_ERR_UNSUPPORTED, "tied embedding format must be F32 or Q4_G32");
+    if (c.wfmt < BH_F32 || c.wfmt > BH_Q4_G32) return ctx->fail(BH_ERR_INVALID, "unknown weight format");
+    const int E = chunk_elems(c.wfmt);
+    const int64_t QD = (int64_t)c.n_heads * c.head_dim, KD = (int64_t)c.n_kv_heads * c.head_dim;
+    if (c.hidden % E || QD % E || c.ffn % E || c.hidden % chunk_elems(c.head_fmt))
+        return ctx->fail(BH_ERR_UNSUPPORTED, "hidden, q_dim and ffn must be multiples of the 16-byte chunk");
+    if (c.max_context > 0 && (c.sink_tokens < 0 || c.sink_tokens >= c.max_context))
+        return ctx->fail(BH_ERR_INVALID, "sink_tokens must be below max_context");
+    if (c.max_tokens > 4096) return ctx->fail(BH_ERR_UNSUPPORTED, "max_tokens above 4096");
+
+    std::lock_guard<std::mutex> g(ctx->mu);
+    bh_model* m = new bh_model();
+    m->ctx = ctx;
+    m->c = c;
+    m->QD = QD;
+    m->KD = KD;
+    m->NQKV = QD + 2 * KD;
+    m->L.resize(c.n_layers);
+    m->max_pos = (int)std::max<int64_t>(65536, c.kv_rows + 1);
+    m->tiles_lm = (int)(pad64(c.vocab) / 64);
+    auto bail = [&](hipError_t e, const char* what) {
+        int rc = ctx->hip_fail(e, what);
+        bh_model_destroy(m);
+        return rc;
+    };
+    hipError_t e = hipStreamCreateWithFlags(&m->st, hipStreamNonBlocking);
+    if (e != hipSuccess) return bail(e, "hipStreamCreate");
+    const size_t kvb = (size_t)c.kv_rows * KD * (c.kv_f16 ? 2 : 4);
+    m->kc.assign(c.n_layers, nullptr);
+    m->vc.assign(c.n_layers, nullptr);
+    for (int l = 0; l < c.n_layers; ++l) {
+        if ((e = dmalloc(m, &m->kc[l], kvb)) != hipSuccess) return bail(e, "hipMalloc(K cache)");
+        if ((e = dmalloc(m, &m->vc[l], kvb)) != hipSuccess) return bail(e, "hipMalloc(V cache)");
+    }
+    const size_t T = (size_t)c.max_tokens;
+    struct {
+        void** p;
+        size_t bytes;
+    } bufs[] = {
+        {(void**)&m->x, T * c.hidden * 4},
+        {(void**)&m->h, T * c.hidden * 4},
+        {(void**)&m->q, T * QD * 4},
+        {(void**)&m->att, T * QD * 4},
+        {(void**)&m->mm, T * c.ffn * 4},
+        {(void**)&m->logits, T * c.vocab * 4},
+        {(void**)&m->part_val, T * m->tiles_lm * 4},
+        {(void**)&m->part_idx, T * m->tiles_lm * 4},
+        {(void**)&m->attn_part, T * c.n_heads * m->max_splits * (c.head_dim + 2) * 4},
+        {(void**)&m->d_tok, T * 4},
+        {(void**)&m->d_pos, T * 4},
+        {(void**)&m->d_slot, T * 4},
+        {(void**)&m->d_ptok, T * 4},
+        {(void**)&m->d_ppos, T * 4},
+        {(void**)&m->d_pslot, T * 4},
+        {(void**)&m->d_next, T * 4},
+        {(void**)&m->d_ids, (size_t)m->ids_steps * T * 4},
+        {(void**)&m->d_step, 16},
+        {(void**)&m->d_seq_len, (size_t)c.max_seqs * 4},
+        {(void**)&m->d_seq_off, (size_t)c.max_seqs * 8},
+        {(void**)&m->d_pen, (size_t)c.max_seqs * c.vocab * 2},
+    };
+    for (auto& b : bufs)
+        if ((e = dmalloc(m, b.p, b.bytes)) != hipSuccess) return bail(e, "hipMalloc(activations)");
+    e = hipHostMalloc((void**)&m->h_stage, (3 * T + 16) * 4, hipHostMallocDefault);
+    if (e != hipSuccess) {
+        m->h_stage = nullptr;
+        return bail(e, "hipHostMalloc");
+    }
+    m->rope = ctx->rope_tab(c.head_dim, c.rope_theta, m->max_pos);
+    if (!m->rope) return bail(hipErrorOutOfMemory, "rope table");
+    m->off_h.assign(c.max_seqs, -1);
+    m->cap_h.assign(c.max_seqs, 0);
+    m->len_h.assign(c.max_seqs, 0);
+    m->open_h.assign(c.max_seqs, 0);
+    *out = m;
+    return BH_OK;
+}
+
+void bh_model_destroy(bh_model* m) {
+    if (!m) return;
+    if (m->st) hipStreamSynchronize(m->st);
+    drop_graph(m);
+    for (auto& w : m->L) {
+        free_weight(w.qkv);
+        free_weight(w.o);
+        free_weight(w.gate);
+        free_weight(w.up);
+        free_weight(w.down);
+    }
+    free_weight(m->embed);
+    for (void* p : m->allocs) hipFree(p);
+    for (auto e : m->ev_pool) hipEventDestroy(e);
+    if (m->h_stage) hipHostFree(m->h_stage);
+    if (m->st) hipStreamDestroy(m->st);
+    delete m;
+}
+
+void* bh_model_stream(bh_model* m) { return m ? (void*)m->st : nullptr; }
+
+int bh_model_set_weight(bh_model* m, const char* name, const void* data, size_t bytes, const void* scales,
+                        size_t scale_bytes) {
+    if (!m || !name) return BH_ERR_INVALID;
+    std::lock_guard<std::mutex> g(m->ctx->mu);
+    const bh_model_config& c = m->c;
+    const int64_t H = c.hidden, I = c.ffn;
+    if (!std::strcmp(name, "model.embed_tokens.weight")) {
+        int rc = ensure_weight(m, m->embed, c.head_fmt, c.vocab, H);
+        if (!rc) rc = upload_rows(m->ctx, m->embed, 0, c.vocab, data, bytes, scales, scale_bytes);
+        if (!rc) m->have_embed = true;
+        return rc;
+    }
+    if (!std::strcmp(name, "model.norm.weight")) {
+        int rc = set_vec(m, &m->norm, H, data, bytes, name);
+        if (!rc) m->have_norm = true;
+        return rc;
+    }
+    int l;
+    const char* r;
+    if (!parse_layer(name, &l, &r) || l < 0 || l >= c.n_layers)
+        return m->fail(BH_ERR_NOT_FOUND, std::string("unknown tensor ") + name);
+    LayerW& w = m->L[l];
+    int rc = BH_ERR_NOT_FOUND, t = -1;
+    if (!std::strcmp(r, "input_layernorm.weight")) { t = T_LN1; rc = set_vec(m, &w.ln1, H, data, bytes, name); }
+    else if (!std::strcmp(r, "post_attention_layernorm.weight")) { t = T_LN2; rc = set_vec(m, &w.ln2, H, data, bytes, name); }
+    else if (!std::strcmp(r, "self_attn.q_proj.weight") || !std::strcmp(r, "self_attn.k_proj.weight") ||
+             !std::strcmp(r, "self_attn.v_proj.weight")) {
+        const int which = r[10] == 'q' ? 0 : (r[10] == 'k' ? 1 : 2);
+        t = T_Q + which;
+        const int64_t row0 = which == 0 ? 0 : (which == 1 ? m->QD : m->QD + m->KD);
+        const int64_t n = which == 0 ? m->QD : m->KD;
+        rc = ensure_weight(m, w.qkv, c.wfmt, m->NQKV, H);
+        if (!rc) rc = upload_rows(m->ctx, w.qkv, row0, n, data, bytes, scales, scale_bytes);
+    } else if (!std::strcmp(r, "self_attn.o_proj.weight")) {
+        t = T_O;
+        rc = ensure_weight(m, w.o, c.wfmt, H, m->QD);
+        if (!rc) rc = upload_rows(m->ctx, w.o, 0, H, data, bytes, scales, scale_bytes);
+    } else if (!std::strcmp(r, "mlp.gate_proj.weight")) {
+        t = T_GATE;
+        rc = ensure_weight(m, w.gate, c.wfmt, I, H);
+        if (!rc) rc = upload_rows(m->ctx, w.gate, 0, I, data, bytes, scales, scale_bytes);
+    } else if (!std::strcmp(r, "mlp.up_proj.weight")) {
+        t = T_UP;
+        rc = ensure_weight(m, w.up, c.wfmt, I, H);
+        if (!rc) rc = upload_rows(m->ctx, w.up, 0, I, data, bytes, scales, scale_bytes);
+    } else if (!std::strcmp(r, "mlp.down_proj.weight")) {
+        t = T_DOWN;
+        rc = ensure_weight(m, w.down, c.wfmt, H, I);
+        if (!rc) rc = upload_rows(m->ctx, w.down, 0, H, data, bytes, scales, scale_bytes);
+    } else if (!std::strcmp(r, "self_attn.q_proj.bias")) { t = T_BQ; rc = set_bias_part(m, w, 0, m->QD, data, bytes, name); }
+    else if (!std::strcmp(r, "self_attn.k_proj.bias")) { t = T_BK; rc = set_bias_part(m, w, m->QD, m->KD, data, bytes, name); }
+    else if (!std::strcmp(r, "self_attn.v_proj.bias")) { t = T_BV; rc = set_bias_part(m, w, m->QD + m->KD, m->KD, data, bytes, name); }
+    else if (!std::strcmp(r, "self_attn.o_proj.bias")) { t = T_BO; rc = set_vec(m, &w.bo, H, data, bytes, name); }
+    else return m->fail(BH_ERR_NOT_FOUND, std::string("unknown tensor ") + name);
+    if (rc == BH_OK) w.have |= 1u << t;
+    return rc;
+}
+
+int bh_model_missing(bh_model* m, int* n_missing) {
+    if (!m || !n_missing) return BH_ERR_INVALID;
+    int miss = (m->have_embed ? 0 : 1) + (m->have_norm ? 0 : 1);
+    for (auto& w : m->L) {
+        uint32_t need = (1u << T_LN1) | (1u << T_LN2) | (1u << T_Q) | (1u << T_K) | (1u << T_V) | (1u << T_O) |
+                        (1u << T_GATE) | (1u << T_UP) | (1u << T_DOWN);
+        if (m->c.attn_bias) need |= (1u << T_BQ) | (1u << T_BK) | (1u << T_BV);
+        if (m->c.o_bias) need |= 1u << T_BO;
+        miss += __builtin_popcount(need & ~w.have);
+    }
+    *n_missing = miss;
+    return BH_OK;
+}
+
+int bh_model_seq_open(bh_model* m, int slot, int64_t capacity) {
+    if (!m) return BH_ERR_INVALID;
+    std::lock_guard<std::mutex> g(m->ctx->mu);
+    if (slot < 0 || slot >= m->c.max_seqs) return m->fail(BH_ERR_INVALID, "slot out of range");
+    if (m->c.max_context > 0) capacity = m->c.max_context;
+    if (capacity <= 0) return m->fail(BH_ERR_INVALID, "capacity must be positive");
+    if (m->off_h[slot] < 0 || m->cap_h[slot] < capacity) {
+        if (m->next_free + capacity > m->c.kv_rows)
+            return m->fail(BH_ERR_CAPACITY, "packed KV buffer full: " + std::to_string(m->next_free) + " + " +
+                                                std::to_string(capacity) + " > " + std::to_string(m->c.kv_rows));
+        m->off_h[slot] = m->next_free;
+        m->cap_h[slot] = capacity;
+        m->next_free += capacity;
+    }
+    m->len_h[slot] = 0;
+    m->open_h[slot] = 1;
+    hipError_t e = hipMemcpyAsync(m->d_seq_off + slot, &m->off_h[slot], 8, hipMemcpyHostToDevice, m->st);
+    const int32_t zero = 0;
+    if (e == hipSuccess) e = hipMemcpyAsync(m->d_seq_len + slot, &zero, 4, hipMemcpyHostToDevice, m->st);
+    if (e == hipSuccess) e = hipMemsetAsync(m->d_pen + (size_t)slot * m->c.vocab, 0, (size_t)m->c.vocab * 2, m->st);
+    if (e == hipSuccess) e = hipStreamSynchronize(m->st);
+    return e == hipSuccess ? BH_OK : m->ctx->hip_fail(e, "seq_open");
+}
+
+int bh_model_prefill(bh_model* m, int slot, const uint32_t* tokens, int n) {
+    if (!m || (n > 0 && !tokens)) return BH_ERR_INVALID;
+    std::lock_guard<std::mutex> g(m->ctx->mu);
+    if (slot < 0 || slot >= m->c.max_seqs || !m->open_h[slot]) return m->fail(BH_ERR_INVALID, "slot is not open");
+    int missing = 0;
+    bh_model_missing(m, &missing);
+    if (missing) return m->fail(BH_ERR_INVALID, std::to_string(missing) + " tensors not set");
+    const int64_t end = m->len_h[slot] + n;
+    if (end > m->max_pos) return m->fail(BH_ERR_CAPACITY, "position beyond the RoPE table");
+    if (m->c.max_context > 0) {
+        if (end > m->c.max_context)
+            return m->fail(BH_ERR_UNSUPPORTED, "prefill past max_context is not supported with eviction");
+    } else if (end > m->cap_h[slot]) {
+        return m->fail(BH_ERR_CAPACITY, "prefill exceeds the slot's KV capacity");
+    }
+    int done = 0;
+    while (done < n) {
+        const int M = std::min(n - done, m->c.max_tokens);
+        int32_t* tok = m->h_stage;
+        int32_t* pos = tok + M;
+        int32_t* sl = pos + M;
+        for (int i = 0; i < M; ++i) {
+            tok[i] = (int32_t)tokens[done + i];
+            pos[i] = m->len_h[slot] + done + i;
+            sl[i] = slot;
+        }
+        hipError_t e = hipMemcpyAsync(m->d_ptok, tok, (size_t)M * 4, hipMemcpyHostToDevice, m->st);
+        if (e == hipSuccess) e = hipMemcpyAsync(m->d_ppos, pos, (size_t)M * 4, hipMemcpyHostToDevice, m->st);
+        if (e == hipSuccess) e = hipMemcpyAsync(m->d_pslot, sl, (size_t)M * 4, hipMemcpyHostToDevice, m->st);
+        int splits, rows;
+        attn_plan(pos[M - 1] + 1, M, m->c.n_kv_heads, &splits, &rows);
+        if (e == hipSuccess) e = forward(m, M, false, splits, rows);
+        if (e == hipSuccess) e = hipStreamSynchronize(m->st);
+        if (e != hipSuccess) return m->ctx->hip_fail(e, "prefill");
+        done += M;
+    }
+    m->len_h[slot] += n;
+    m->h_stage[0] = m->len_h[slot];
+    hipError_t e = hipMemcpyAsync(m->d_seq_len + slot, m->h_stage, 4, hipMemcpyHostToDevice, m->st);
+    if (e == hipSuccess) e = hipStreamSynchronize(m->st);
+    return e == hipSuccess ? BH_OK : m->ctx->hip_fail(e, "prefill");
+}
+
+int bh_model_decode_setup(bh_model* m, int batch, const int32_t* slots, const uint32_t* first_tokens) {
+    if (!m || batch <= 0 || !slots || !first_tokens) return BH_ERR_INVALID;
+    std::lock_guard<std::mutex> g(m->ctx->mu);
+    if (batch > m->c.max_tokens) return m->fail(BH_ERR_CAPACITY, "decode batch above max_tokens");
+    std::vector<int32_t> seen(m->c.max_seqs, 0);
+    for (int b = 0; b < batch; ++b) {
+        if (slots[b] < 0 || slots[b] >= m->c.max_seqs || !m->open_h[slots[b]])
+            return m->fail(BH_ERR_INVALID, "decode slot is not open");
+        if (seen[slots[b]]++) return m->fail(BH_ERR_INVALID, "a slot appears twice in the decode batch");
+    }
+    if (batch != m->B) drop_graph(m);
+    m->B = batch;
+    m->bslots.assign(slots, slots + batch);
+    hipError_t e = hipMemcpyAsync(m->d_slot, slots, (size_t)batch * 4, hipMemcpyHostToDevice, m->st);
+    if (e == hipSuccess) e = hipMemcpyAsync(m->d_next, first_tokens, (size_t)batch * 4, hipMemcpyHostToDevice, m->st);
+    if (e == hipSuccess) e = hipStreamSynchronize(m->st);
+    return e == hipSuccess ? BH_OK : m->ctx->hip_fail(e, "decode_setup");
+}
+
+int bh_model_decode_replace(bh_model* m, int b, int slot, uint32_t first_token) {
+    if (!m) return BH_ERR_INVALID;
+    std::lock_guard<std::mutex> g(m->ctx->mu);
+    if (b < 0 || b >= m->B) return m->fail(BH_ERR_INVALID, "batch entry out of range");
+    if (slot < 0 || slot >= m->c.max_seqs || !m->open_h[slot]) return m->fail(BH_ERR_INVALID, "slot is not open");
+    for (int i = 0; i < m->B; ++i)
+        if (i != b && m->bslots[i] == slot) return m->fail(BH_ERR_INVALID, "slot already in the batch");
+    m->bslots[b] = slot;
+    m->h_stage[0] = slot;
+    m->h_stage[1] = (int32_t)first_token;
+    hipError_t e = hipMemcpyAsync(m->d_slot + b, &m->h_stage[0], 4, hipMemcpyHostToDevice, m->st);
+    if (e == hipSuccess) e = hipMemcpyAsync(m->d_next + b, &m->h_stage[1], 4, hipMemcpyHostToDevice, m->st);
+    if (e == hipSuccess) e = hipStreamSynchronize(m->st);
+    return e == hipSuccess ? BH_OK : m->ctx->hip_fail(e, "decode_replace");
+}
+
+static int decode_locked(bh_model* m, int n_steps, uint32_t* ids_out, float* raw_logits) {
+    if (m->B <= 0) return m->fail(BH_ERR_INVALID, "no decode batch (bh_model_decode_setup)");
+    int missing = 0;
+    bh_model_missing(m, &missing);
+    if (missing) return m->fail(BH_ERR_INVALID, std::to_string(missing) + " tensors not set");
+    int rc = check_decode_room(m, n_steps);
+    if (rc) return rc;
+    int splits, rows;
+    attn_plan(decode_len_bound(m, n_steps), m->B, m->c.n_kv_heads, &splits, &rows);
+    hipError_t e = hipSuccess;
+    if (!m->gexec || m->g_B != m->B || m->g_splits != splits || m->g_rows != rows) {
+        drop_graph(m);
+        e = hipStreamBeginCapture(m->st, hipStreamCaptureModeThreadLocal);
+        if (e != hipSuccess) return m->ctx->hip_fail(e, "hipStreamBeginCapture");
+        hipError_t fe = forward(m, m->B, true, splits, rows);
+        e = hipStreamEndCapture(m->st, &m->graph);
+        if (fe != hipSuccess) e = fe;
+        if (e == hipSuccess) e = hipGraphInstantiate(&m->gexec, m->graph, nullptr, nullptr, 0);
+        if (e != hipSuccess) {
+            drop_graph(m);
+            return m->ctx->hip_fail(e, "decode graph capture");
+        }
+        m->g_B = m->B;
+        m->g_splits = splits;
+        m->g_rows = rows;
+    }
+    int done = 0;
+    while (done < n_steps && e == hipSuccess) {
+        const int chunk = (int)std::min<int64_t>(n_steps - done, m->ids_steps);
+        e = launch_step_counter(m->d_step, 1, m->st);
+        for (int s = 0; s < chunk && e == hipSuccess; ++s) {
+            e = hipGraphLaunch(m->gexec, m->st);
+            if (e == hipSuccess && raw_logits)
+                e = hipMemcpyAsync(raw_logits + (size_t)(done + s) * m->B * m->c.vocab, m->logits,
+                                   (size_t)m->B * m->c.vocab * 4, hipMemcpyDeviceToHost, m->st);
+        }
+        if (e == hipSuccess && ids_out)
+            e = hipMemcpyAsync(ids_out + (size_t)done * m->B, m->d_ids, (size_t)chunk * m->B * 4,
+                               hipMemcpyDeviceToHost, m->st);
+        if (e == hipSuccess) e = hipStreamSynchronize(m->st);
+        done += chunk;
+    }
+    if (e != hipSuccess) return m->ctx->hip_fail(e, "decode");
+    for (int b = 0; b < m->B; ++b) m->len_h[m->bslots[b]] += n_steps;
+    return BH_OK;
+}
+
+int bh_model_decode(bh_model* m, int n_steps, uint32_t* ids_out, float* raw_logits) {
+    if (!m || n_steps < 0) return BH_ERR_INVALID;
+    std::lock_guard<std::mutex> g(m->ctx->mu);
+    int st;
+    if (m->ctx->injected(BH_OP_DECODE, &st)) return st;
+    if (n_steps == 0) return BH_OK;
+    return decode_locked(m, n_steps, ids_out, raw_logits);
+}
+
+int bh_model_generate(bh_model* m, int slot, const uint32_t* prompt, int n_prompt, int max_new, uint32_t* ids_out,
+                      int* n_out, float* raw_logits) {
+    if (!m || n_prompt < 0 || max_new < 0 || (n_prompt > 0 && !prompt) || !n_out || (max_new > 0 && !ids_out))
+        return BH_ERR_INVALID;
+    *n_out = 0;
+    std::vector<uint32_t> toks(prompt, prompt + n_prompt);
+    if (toks.empty()) toks.push_back(1);  // cpu_engine.rs:2487-2489
+    const int64_t need = (int64_t)toks.size() + max_new;
+    int rc = bh_model_seq_open(m, slot, need);
+    if (rc) return rc;
+    rc = bh_model_prefill(m, slot, toks.data(), (int)toks.size() - 1);
+    if (rc) return rc;
+    const int32_t s = slot;
+    const uint32_t last = toks.back();
+    rc = bh_model_decode_setup(m, 1, &s, &last);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> g(m->ctx->mu);
+    int got = 0;
+    const int chunk = 16;
+    std::vector<uint32_t> ids(chunk);
+    while (got < max_new) {
+        const int n = std::min(chunk, max_new - got);
+        rc = decode_locked(m, n, ids.data(), raw_logits ? raw_logits + (size_t)got * m->c.vocab : nullptr);
+        if (rc) return rc;
+        bool eos = false;
+        for (int i = 0; i < n; ++i) {
+            ids_out[got++] = ids[i];
+            if (ids[i] == 2 || ids[i] == 151645 || ids[i] == 151643) {  // cpu_engine.rs:3060
+                eos = true;
+                break;
+            }
+        }
+        if (eos) break;
+    }
+    *n_out = got;
+    return BH_OK;
+}
+
+int bh_model_time_kernels(bh_model* m, int n_steps, double* mean_us, int64_t* launches) {
+    if (!m || n_steps <= 0 || !mean_us || !launches) return BH_ERR_INVALID;
+    std::lock_guard<std::mutex> g(m->ctx->mu);
+    if (m->B <= 0) return m->fail(BH_ERR_INVALID, "no decode batch");
+    if (n_steps > m->ids_steps) return m->fail(BH_ERR_INVALID, "at most 1024 timed steps per call");
+    int rc = check_decode_room(m, n_steps);
+    if (rc) return rc;
+    int splits, rows;
+    attn_plan(decode_len_bound(m, n_steps), m->B, m->c.n_kv_heads, &splits, &rows);
+    std::vector<double> tot(BH_K_COUNT, 0.0);
+    std::vector<int64_t> cnt(BH_K_COUNT, 0);
+    hipError_t e = launch_step_counter(m->d_step, 1, m->st);
+    for (int s = 0; s < n_steps && e == hipSuccess; ++s) {
+        m->timing = true;
+        m->recs.clear();
+        m->ev_used = 0;
+        e = forward(m, m->B, true, splits, rows);
+        m->timing = false;
+        if (e == hipSuccess) e = hipStreamSynchronize(m->st);
+        for (auto& r : m->recs) {
+            float ms = 0.f;
+            if (hipEventElapsedTime(&ms, r.a, r.b) == hipSuccess) {
+                tot[r.cls] += ms * 1000.0;
+                cnt[r.cls] += 1;
+            }
+        }
+    }
+    if (e != hipSuccess) return m->ctx->hip_fail(e, "timed decode");
+    for (int b = 0; b < m->B; ++b) m->len_h[m->bslots[b]] += n_steps;
+    for (int k = 0; k < BH_K_COUNT; ++k) {
+        mean_us[k] = cnt[k] ? tot[k] / cnt[k] : 0.0;
+        launches[k] = cnt[k];
+    }
+    return BH_OK;
+}
+
+int bh_model_kernel_bytes(bh_model* m, int kclass, double* bytes) {
+    if (!m || !bytes) return BH_ERR_INVALID;
+    const bh_model_config& c = m->c;
+    const double B = m->B > 0 ? m->B : 1, H = c.hidden, I = c.ffn, QD = (double)m->QD, KD = (double)m->KD;
+    const double kvb = c.kv_f16 ? 2.0 : 4.0;
+    const LayerW& w = m->L[0];
+    switch (kclass) {
+        case BH_K_GEMV_QKV:
+            *bytes = weight_bytes(w.qkv) + (c.attn_bias ? (QD + 2 * KD) * 4 : 0) + B * H * 4 + B * QD * 4 +
+                     B * 2 * KD * kvb;
+            return BH_OK;
+        case BH_K_GEMV_O: *bytes = weight_bytes(w.o) + B * QD * 4 + 2 * B * H * 4; return BH_OK;
+        case BH_K_GEMV_GATEUP: *bytes = weight_bytes(w.gate) + weight_bytes(w.up) + B * H * 4 + B * I * 4; return BH_OK;
+        case BH_K_GEMV_DOWN: *bytes = weight_bytes(w.down) + B * I * 4 + 2 * B * H * 4; return BH_OK;
+        case BH_K_LM_HEAD:
+            *bytes = weight_bytes(m->embed) + B * H * 4 + B * (double)c.vocab * 4 + B * (double)c.vocab * 2;
+            return BH_OK;
+        case BH_K_ATTN: {
+            double rows = 0;
+            for (int b = 0; b < m->B; ++b) {
+                int64_t len = m->len_h[m->bslots[b]];
+                if (c.max_context > 0) len = std::min<int64_t>(len, c.max_context);
+                rows += (double)len;
+            }
+            *bytes = rows * 2 * KD * kvb + 2 * B * QD * 4;
+            return BH_OK;
+        }
+        case BH_K_NORM: *bytes = 2 * B * H * 4 + H * 4; return BH_OK;
+        default: *bytes = 0; return BH_OK;
+    }
+}
+
+}  // extern "C"

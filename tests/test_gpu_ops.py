@@ -1,0 +1,212 @@
+"""GPU parity of the single operators against the oracle (and float64 where the oracle
+is itself float32). Tolerances are stated per test."""
+import numpy as np
+import pytest
+
+import oracle
+import ref64
+from bramha_amd import _lib, ops
+from bramha_amd._lib import BH_F32, BH_Q4_G32, BH_Q4_ROW, BH_Q8_ROW, BhError
+from bramha_amd.plane import try_gpu_matvec
+
+pytestmark = pytest.mark.gpu
+
+QWEN_SHAPES = [(896, 896), (128, 896), (4864, 896), (896, 4864), (151936, 896)]  # (N, K)
+
+
+def _quant(fmt, w):
+    if fmt == BH_F32:
+        return w, None, w
+    if fmt == BH_Q8_ROW:
+        q, s = oracle.quantize_int8(w)
+        return q, s, oracle.dequantize_int8(q, s)
+    if fmt == BH_Q4_ROW:
+        q, s = oracle.quantize_int4(w)
+        return q, s, oracle.dequantize_int4(q, s, w.shape[1])
+    q, s = oracle.quantize_q4g32(w)
+    return q, s, oracle.dequantize_q4g32(q, s, w.shape[1])
+
+
+def _w(seed, n, k, sigma=0.02):
+    return (np.random.default_rng(seed).standard_normal((n, k)) * sigma).astype(np.float32)
+
+
+@pytest.mark.parametrize("fmt", [BH_F32, BH_Q8_ROW, BH_Q4_ROW, BH_Q4_G32])
+@pytest.mark.parametrize("n,k", [(64, 128), (37, 96), (896, 896), (4864, 896), (896, 4864)])
+def test_dequant_bit_exact(plane, fmt, n, k):
+    w = _w(n + k, n, k)
+    w[0] = 0
+    q, s, deq = _quant(fmt, w)
+    dw = ops.DeviceWeight(plane, fmt, n, k, q, s)
+    got = dw.dequant().cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), deq.view(np.uint32))
+
+
+def test_dequant_bit_exact_lm_head(plane):
+    w = _w(9, 151936, 896)
+    q, s, deq = _quant(BH_Q4_G32, w)
+    got = ops.DeviceWeight(plane, BH_Q4_G32, 151936, 896, q, s).dequant().cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), deq.view(np.uint32))
+
+
+def _check_gemv(y, deq, x):
+    """Within f32 accumulation error of the exact product: |y - y64| <= 2e-6 * (|W| |x|) + 1e-7."""
+    want = x.astype(np.float64) @ deq.astype(np.float64).T
+    bound = 2e-6 * (np.abs(x).astype(np.float64) @ np.abs(deq).astype(np.float64).T) + 1e-7
+    err = np.abs(y - want)
+    assert np.all(err <= bound), float((err / bound).max())
+
+
+_QCACHE = {}
+
+
+def _q4_cached(n, k):
+    if (n, k) not in _QCACHE:
+        _QCACHE.clear()
+        _QCACHE[(n, k)] = _quant(BH_Q4_G32, _w(n * 7 + k, n, k))
+    return _QCACHE[(n, k)]
+
+
+@pytest.mark.parametrize("n,k", QWEN_SHAPES)
+@pytest.mark.parametrize("batch", [1, 4, 16, 32])
+def test_gemv_q4g32_qwen_shapes(plane, n, k, batch):
+    import torch
+
+    q, s, deq = _q4_cached(n, k)
+    x = np.random.default_rng(batch).standard_normal((batch, k)).astype(np.float32)
+    dw = ops.DeviceWeight(plane, BH_Q4_G32, n, k, q, s)
+    y = dw.gemv(torch.from_numpy(x).cuda()).cpu().numpy()
+    _check_gemv(y, deq, x)
+    if batch == 1:  # the reference GEMV over the dequantized weights
+        yo = oracle.matvec_mul_into(oracle.F32, x[0], deq, None, n)
+        assert np.max(np.abs(y[0] - yo)) <= 1e-5 * max(1.0, np.abs(yo).max())
+
+
+@pytest.mark.parametrize("fmt", [BH_F32, BH_Q8_ROW, BH_Q4_ROW])
+@pytest.mark.parametrize("n,k,batch", [(896, 896, 1), (4864, 896, 3), (896, 4864, 8), (300, 96, 5)])
+def test_gemv_row_formats(plane, fmt, n, k, batch):
+    import torch
+
+    w = _w(fmt * 31 + n, n, k)
+    q, s, deq = _quant(fmt, w)
+    x = np.random.default_rng(n).standard_normal((batch, k)).astype(np.float32)
+    y = ops.DeviceWeight(plane, fmt, n, k, q, s).gemv(torch.from_numpy(x).cuda()).cpu().numpy()
+    _check_gemv(y, deq, x)
+    yo = oracle.matvec_mul_into(fmt, x[0], q, s, n)
+    assert np.max(np.abs(y[0] - yo)) <= 1e-5 * max(1.0, np.abs(yo).max())
+
+
+def test_matvec_mirror_reference_vectors(plane):
+    # test_wgpu_gemv_vs_cpu (wgpu_backend.rs:1734-1782): GPU == CPU within 1e-4
+    h = (np.arange(128, dtype=np.float32) * np.float32(0.01)).astype(np.float32)
+    w = (np.arange(128 * 64, dtype=np.float32) * np.float32(0.0001)).astype(np.float32)
+    gpu = plane.matvec_mul(h, w, 64)
+    cpu = oracle.matvec_mul(oracle.F32, h, w.reshape(64, 128), None, 64)
+    assert np.max(np.abs(gpu - cpu)) < 1e-4
+    # test_quantization_correctness GPU branch (cpu_engine.rs:3649-3681)
+    i = np.arange(64 * 128, dtype=np.float32)
+    wq = (np.cos(i * np.float32(0.17)) * np.float32(0.5)).astype(np.float32).reshape(64, 128)
+    hq = np.sin(np.arange(128, dtype=np.float32) * np.float32(0.31)).astype(np.float32)
+    q8, s8 = oracle.quantize_int8(wq)
+    assert np.max(np.abs(plane.matvec_mul_int8(hq, q8, s8, 64) - oracle.matvec_mul(oracle.Q8_ROW, hq, q8, s8, 64))) < 1e-4
+    q4, s4 = oracle.quantize_int4(wq)
+    assert np.max(np.abs(plane.matvec_mul_int4(hq, q4, s4, 64) - oracle.matvec_mul(oracle.Q4_ROW, hq, q4, s4, 64))) < 1e-4
+
+
+def test_registry_errors_and_faults(plane):
+    plane.clear_persistent_buffers()
+    rng = np.random.default_rng(0)
+    h = rng.standard_normal(896).astype(np.float32)
+    w = _w(1, 896, 896)
+    q, s = oracle.quantize_int4(w)
+    want = oracle.matvec_mul_into(oracle.Q4_ROW, h, q, s, 896)
+    y1 = plane.matvec_mul_int4(h, q, s, 896, "m", "layer.0")
+    assert plane.registry_stats()[0] == 1
+    # same key: the cached weight is used, the new argument's contents are ignored (get_or_create_op)
+    y2 = plane.matvec_mul_int4(h, np.zeros_like(q), s, 896, "m", "layer.0")
+    assert np.array_equal(y1, y2) and np.max(np.abs(y1 - want)) < 1e-4
+    # same key, other shape: an error, not a wrong answer
+    with pytest.raises(BhError):
+        plane.matvec_mul_int4(h[:128], q[:, :64], s, 896, "m", "layer.0")
+    # unkeyed calls do not register
+    plane.matvec_mul_int4(h, q, s, 896)
+    assert plane.registry_stats()[0] == 1
+    # LRU eviction under the cap
+    _, one = plane.registry_stats()
+    plane.set_vram_cap(2 * one)
+    plane.matvec_mul_int4(h, q, s, 896, "m", "layer.1")
+    plane.matvec_mul_int4(h, q, s, 896, "m", "layer.0")  # touch 0: layer.1 is now oldest
+    plane.matvec_mul_int4(h, q, s, 896, "m", "layer.2")
+    n, b = plane.registry_stats()
+    assert n == 2 and b <= 2 * one
+    plane.set_vram_cap(64 << 30)
+    plane.clear_persistent_buffers()
+    assert plane.registry_stats() == (0, 0)
+    # size mismatch -> Err(String) (wgpu_backend.rs:1096-1104)
+    with pytest.raises(BhError, match="size mismatch"):
+        plane.matvec_mul_int4(h, q[:-1], s, 896)
+    # empty input -> Ok(zeros)
+    assert np.array_equal(plane.matvec_mul(np.zeros(0, np.float32), np.zeros(0, np.float32), 5), np.zeros(5))
+    # injected fault: the call fails without side effects, the next one succeeds, and the
+    # dispatch seam hands the work back to the caller's CPU path
+    plane.inject_fault(_lib.BH_OP_MATVEC, _lib.BH_ERR_INJECTED, 1)
+    assert try_gpu_matvec(h, "int4", q, s, 896, plane=plane) is None
+    assert np.max(np.abs(try_gpu_matvec(h, "int4", q, s, 896, plane=plane) - want)) < 1e-4
+
+
+def test_rmsnorm_rope_silu(plane):
+    import torch
+
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((5, 896)) * 3).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(896)).astype(np.float32)
+    got = ops.rmsnorm(plane, torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda(), 1e-6).cpu().numpy()
+    want = np.stack([oracle.rms_norm(r, w, 1e-6) for r in x])
+    assert np.max(np.abs(got - want)) < 1e-5 * np.abs(want).max()
+    pos = np.array([0, 1, 31, 4095, 32767], np.int32)
+    v = rng.standard_normal((5, 14 * 64)).astype(np.float32)
+    vt = torch.from_numpy(v).cuda()
+    ops.rope_(plane, vt, torch.from_numpy(pos).cuda(), 14, 64, 1e6, 40960)
+    got = vt.cpu().numpy()
+    for i, p in enumerate(pos):
+        want = oracle.apply_rope(v[i], int(p), 14, 64, 1e6)
+        assert np.max(np.abs(got[i] - want)) < 2e-6 * max(1.0, np.abs(want).max()), p
+    g = (rng.standard_normal(4864) * 3).astype(np.float32)
+    u = rng.standard_normal(4864).astype(np.float32)
+    got = ops.silu_mul(plane, torch.from_numpy(g).cuda(), torch.from_numpy(u).cuda()).cpu().numpy()
+    want = oracle.silu_mul(g, u)
+    assert np.max(np.abs(got - want)) < 2e-6 * np.abs(want).max()
+
+
+def _attn_case(plane, lens, nq=14, nkv=2, hd=64, kv_f16=True, seed=0, check_rows=None):
+    import torch
+
+    rng = np.random.default_rng(seed)
+    B = len(lens)
+    offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)  # prefix sums
+    rows = int(np.sum(lens))
+    kdt = np.float16 if kv_f16 else np.float32
+    k = rng.standard_normal((nkv, rows, hd)).astype(kdt)
+    v = rng.standard_normal((nkv, rows, hd)).astype(kdt)
+    q = rng.standard_normal((B, nq * hd)).astype(np.float32)
+    out = ops.attn_decode(plane, torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                          torch.from_numpy(offs).cuda(), torch.from_numpy(np.array(lens, np.int32)).cuda(), nq, nkv,
+                          hd, int(max(lens))).cpu().numpy()
+    for b in (check_rows if check_rows is not None else range(B)):
+        kc = k[:, offs[b]:offs[b] + lens[b]].astype(np.float32).transpose(1, 0, 2)  # -> [T][nkv][hd]
+        vc = v[:, offs[b]:offs[b] + lens[b]].astype(np.float32).transpose(1, 0, 2)
+        want = oracle.attn_decode(q[b], kc, vc, lens[b], nq, nkv, hd)
+        assert np.max(np.abs(out[b] - want)) < 2e-5, (b, lens[b])
+
+
+@pytest.mark.parametrize("T", [512, 4096, 32768])
+@pytest.mark.parametrize("B", [1, 8])
+def test_attention_config3(plane, T, B):
+    # GQA 14 q / 2 kv heads, head_dim 64, fp16 K/V N(0,1), one query token, contexts 512/4096/32768
+    _attn_case(plane, [T] * B, seed=T + B, check_rows=[0, B - 1])
+
+
+def test_attention_ragged_and_short(plane):
+    _attn_case(plane, [1, 2, 63, 64, 65, 200, 257, 1000], seed=1)
+    _attn_case(plane, [5, 300], kv_f16=False, seed=2)
+    _attn_case(plane, [130, 7], nq=28, nkv=4, hd=128, seed=3)  # Qwen2-7B heads
