@@ -47,13 +47,13 @@ def build_model(plane, batch, prompt_len, steps_total, seed=0):
 
 
 def timed_decode(m, steps, warmup):
-    import torch
+    from bramha_amd import ops
 
     m.decode(warmup)
-    torch.cuda.synchronize()
+    ops.synchronize(m.plane)
     t0 = time.perf_counter()
     m.decode(steps)
-    torch.cuda.synchronize()
+    ops.synchronize(m.plane)
     return time.perf_counter() - t0
 
 
@@ -121,8 +121,6 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
-    import torch
-
     from bramha_amd.plane import HipComputePlane
 
     plane = HipComputePlane(0)
@@ -172,7 +170,6 @@ def main():
     }
     print(json.dumps(line), flush=True)
     plane.close()
-    torch.cuda.synchronize()
 
 
 if __name__ == "__main__":

@@ -12,7 +12,7 @@ LIB_PATH = os.path.join(HERE, "libbramha_hip.so")
 
 if not os.path.exists(LIB_PATH):
     raise ImportError(
-        "bramha_amd: %s is missing; build it with `python -m bramha_amd.build` "
+        "bramha_amd: %s is missing; build it with `python bramha_amd/build.py` "
         "(or __graft_entry__.build())" % LIB_PATH
     )
 
@@ -73,6 +73,11 @@ _PROTOS = {
     "bh_set_vram_cap": (c_int, [_P, c_size_t]),
     "bh_registry_stats": (c_int, [_P, POINTER(c_size_t), POINTER(c_size_t)]),
     "bh_debug_inject_fault": (c_int, [_P, c_int, c_int, c_int]),
+    "bh_dev_alloc": (c_int, [_P, c_size_t, POINTER(c_void_p)]),
+    "bh_dev_free": (c_int, [_P, _P]),
+    "bh_memcpy_h2d": (c_int, [_P, _P, _P, c_size_t]),
+    "bh_memcpy_d2h": (c_int, [_P, _P, _P, c_size_t]),
+    "bh_synchronize": (c_int, [_P]),
     "bh_matvec_mul": (c_int, [_P, _P, c_size_t, _P, c_size_t, c_size_t, c_char_p, c_char_p, _P]),
     "bh_matvec_mul_int8": (c_int, [_P, _P, c_size_t, _P, c_size_t, _P, c_size_t, c_size_t, c_char_p, c_char_p, _P]),
     "bh_matvec_mul_int4": (c_int, [_P, _P, c_size_t, _P, c_size_t, _P, c_size_t, c_size_t, c_char_p, c_char_p, _P]),

@@ -2,7 +2,7 @@
 
 Every source is compiled with hipcc for gfx950 only, in parallel, then linked into
 one shared library that exports the C ABI of include/bramha_hip.h.
-Run: python -m bramha_amd.build   (or call build()).
+Run: python bramha_amd/build.py   (by path: importing the package loads the library).
 """
 import os
 import subprocess

@@ -7,6 +7,7 @@
 // get_or_create_op, :603-722). Its matvec_mul* methods keep the reference's
 // argument meaning and error behaviour: empty input -> Ok(zeros), size
 // mismatch -> Err(text), everything else -> Ok(result).
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -310,6 +311,7 @@ void bh_destroy(bh_ctx* ctx) {
     if (ctx->d_y) hipFree(ctx->d_y);
     for (auto& kv : ctx->rope_tabs) hipFree(kv.second);
     if (ctx->attn_part) hipFree(ctx->attn_part);
+    if (ctx->attn_cnt) hipFree(ctx->attn_cnt);
     hipStreamDestroy(ctx->stream);
     delete ctx;
 }
@@ -339,6 +341,47 @@ int bh_debug_inject_fault(bh_ctx* ctx, int op, int status, int count) {
     ctx->inj_status = status == 0 ? BH_ERR_INJECTED : status;
     ctx->inj_count = count;
     return BH_OK;
+}
+
+int bh_dev_alloc(bh_ctx* ctx, size_t bytes, void** out) {
+    if (!ctx || !out) return BH_ERR_INVALID;
+    *out = nullptr;
+    hipError_t e = hipMalloc(out, std::max<size_t>(bytes, 1));
+    if (e != hipSuccess) {
+        *out = nullptr;
+        return ctx->hip_fail(e, "hipMalloc");
+    }
+    return BH_OK;
+}
+
+int bh_dev_free(bh_ctx* ctx, void* p) {
+    if (!ctx) return BH_ERR_INVALID;
+    if (!p) return BH_OK;
+    hipStreamSynchronize(ctx->stream);
+    hipError_t e = hipFree(p);
+    return e == hipSuccess ? BH_OK : ctx->hip_fail(e, "hipFree");
+}
+
+int bh_memcpy_h2d(bh_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    if (!ctx || (bytes && (!dst || !src))) return BH_ERR_INVALID;
+    if (!bytes) return BH_OK;
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    return e == hipSuccess ? BH_OK : ctx->hip_fail(e, "hipMemcpy H2D");
+}
+
+int bh_memcpy_d2h(bh_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    if (!ctx || (bytes && (!dst || !src))) return BH_ERR_INVALID;
+    if (!bytes) return BH_OK;
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    return e == hipSuccess ? BH_OK : ctx->hip_fail(e, "hipMemcpy D2H");
+}
+
+int bh_synchronize(bh_ctx* ctx) {
+    if (!ctx) return BH_ERR_INVALID;
+    hipError_t e = hipDeviceSynchronize();
+    return e == hipSuccess ? BH_OK : ctx->hip_fail(e, "hipDeviceSynchronize");
 }
 
 int bh_matvec_mul(bh_ctx* ctx, const float* h, size_t in_features, const float* weight, size_t weight_len,
@@ -478,9 +521,8 @@ int bh_attn_decode(bh_ctx* ctx, const float* q, const void* k, const void* v, in
     if (!ctx || !q || !k || !v || !seq_off || !seq_len || !out || batch < 0 || n_q <= 0 || n_kv <= 0 ||
         n_q % n_kv || max_len < 0)
         return BH_ERR_INVALID;
-    if (head_dim != 64 && head_dim != 128)
-        return ctx->fail(BH_ERR_UNSUPPORTED, "attention supports head_dim 64 and 128");
-    if (n_q / n_kv > 8) return ctx->fail(BH_ERR_UNSUPPORTED, "attention supports up to 8 query heads per KV head");
+    if (!attn_supported(n_q, n_kv, head_dim))
+        return ctx->fail(BH_ERR_UNSUPPORTED, "attention supports head_dim 64/128 and 1, 2, 4, 7 or 8 query heads per KV head");
     if (batch == 0) return BH_OK;
     std::lock_guard<std::mutex> g(ctx->mu);
     AttnArgs a;
@@ -509,6 +551,16 @@ int bh_attn_decode(bh_ctx* ctx, const float* q, const void* k, const void* v, in
         }
         a.part_o = (float*)ctx->attn_part;
         a.part_ml = a.part_o + (size_t)batch * n_q * a.splits * head_dim;
+        if (batch * n_kv > ctx->attn_cnt_len) {
+            if (ctx->attn_cnt) hipFree(ctx->attn_cnt);
+            ctx->attn_cnt = nullptr;
+            ctx->attn_cnt_len = 0;
+            hipError_t e = hipMalloc((void**)&ctx->attn_cnt, (size_t)batch * n_kv * 4);
+            if (e == hipSuccess) e = hipMemset(ctx->attn_cnt, 0, (size_t)batch * n_kv * 4);
+            if (e != hipSuccess) return ctx->hip_fail(e, "hipMalloc(attention counters)");
+            ctx->attn_cnt_len = batch * n_kv;
+        }
+        a.cnt = ctx->attn_cnt;
     }
     hipError_t e = launch_attention(a, pick(ctx, stream));
     return e == hipSuccess ? BH_OK : ctx->hip_fail(e, "attention launch");

@@ -33,6 +33,8 @@ struct bh_ctx {
     size_t y_cap = 0;
     void* attn_part = nullptr;
     size_t attn_part_bytes = 0;
+    int32_t* attn_cnt = nullptr;  // split-merge counters, zero when idle
+    int attn_cnt_len = 0;
     std::unordered_map<std::string, void*> rope_tabs;
 
     // Fault injection (bh_debug_inject_fault).

@@ -52,6 +52,7 @@ enum Epi : int {
     EPI_SILU = 2,    // y = silu(acc_gate) * acc_up (gate/up pair)
     EPI_QKV = 3,     // bias, RoPE, q -> y, k/v -> KV cache
     EPI_LMHEAD = 4,  // logits -> y, repetition penalty, per-tile argmax -> partial
+    EPI_PART = 5,    // K split over workgroups: scaled partial sums -> part[split][b][n]
 };
 
 struct KvView {            // packed KV cache of one layer
@@ -87,6 +88,11 @@ struct GemvArgs {
     int vocab = 0;
     float* part_val = nullptr;         // [batch][tiles]
     int32_t* part_idx = nullptr;
+    // EPI_PART: `ksw` workgroups per row tile each write their scaled partial sums to
+    // part[split][b][n] (stride part_ld per split, N per row); the consumer adds them.
+    float* part = nullptr;
+    int ksw = 1;
+    int64_t part_ld = 0;
 };
 
 // Launchers (k_gemv.hip). Return hipSuccess or the launch error.
@@ -94,6 +100,12 @@ hipError_t launch_gemv(int fmt, int epi, const GemvArgs& a, hipStream_t st);
 
 // k_ops.hip
 hipError_t launch_rmsnorm(const float* x, const float* w, float eps, float* out, int rows, int n, hipStream_t st);
+// Residual reduce + RMSNorm per row b: x[b] += sum_{s < splits} part[s][b] (+ bias), in a
+// fixed order, then h[b] = x[b] * (1/sqrt(mean(x[b]^2) + eps)) * w. splits 0: norm only.
+hipError_t launch_resid_norm(float* x, const float* part, int splits, int64_t part_ld, const float* bias,
+                             const float* w, float eps, float* h, int rows, int n, hipStream_t st);
+// Split count for an EPI_PART GEMV over `tiles` row tiles and C chunks.
+int part_splits(int tiles, int C);
 hipError_t launch_rope(float* v, const int32_t* pos, const float2* tab, int rows, int n_heads, int hd, hipStream_t st);
 hipError_t launch_silu_mul(const float* g, const float* u, float* out, int64_t n, hipStream_t st);
 hipError_t launch_dequant(const DevWeight& w, float* out, hipStream_t st);
@@ -112,6 +124,7 @@ hipError_t launch_step_counter(int32_t* ctr, int reset, hipStream_t st);
 // rows present for its sequence after its own row was appended.
 struct AttnArgs {
     const float* q = nullptr;  // [batch][nq*hd]
+    int32_t* cnt = nullptr;    // [batch][nkv] arrival counters of the split merge (zero when idle)
     float* out = nullptr;      // [batch][nq*hd]
     KvView kv;
     const int32_t* pos = nullptr;
@@ -124,6 +137,8 @@ struct AttnArgs {
     float* part_ml = nullptr;          // [batch][nq][splits][2]
 };
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
+// Head layouts the attention kernel is built for: hd 64/128, n_q/n_kv in {1, 2, 4, 7, 8}.
+bool attn_supported(int nq, int nkv, int hd);
 // Split plan for contexts up to max_len rows.
 void attn_plan(int max_len, int batch, int nkv, int* splits, int* split_rows);
 

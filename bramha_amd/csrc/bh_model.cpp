@@ -56,6 +56,9 @@ struct bh_model {
     int32_t* part_idx = nullptr;
     float* attn_part = nullptr;
     int max_splits = 128;
+    int32_t* attn_cnt = nullptr;   // [max_tokens][n_kv] split-merge counters
+    float* gemv_part = nullptr;    // split-K partial sums of the O / down projections
+    int64_t part_ld = 0;           // floats per split: max_tokens * hidden
     // decode batch inputs (read by the captured graph) and prefill inputs, kept apart so a
     // prefill between decode calls leaves the batch intact
     int32_t *d_tok = nullptr, *d_pos = nullptr, *d_slot = nullptr;
@@ -135,6 +138,8 @@ KvView kv_view(bh_model* m, int l) {
 
 // One forward pass over M tokens: the decode batch (decode = true: tokens from the last
 // argmax, positions from the row counts, logits and sampling) or a staged prefill chunk.
+// Per layer: QKV (+bias, RoPE, KV append) -> attention -> O partial sums -> residual +
+// post-attention norm -> gate/up + SiLU -> down partial sums -> residual + next norm.
 hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) {
     const bh_model_config& c = m->c;
     const int H = c.hidden, I = c.ffn;
@@ -146,10 +151,12 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
     hipError_t e = timed(m, BH_K_OTHER, [&] {
         return launch_embed(m->embed, tok, pos, slot, m->d_seq_len, m->d_next, decode ? 1 : 0, m->x, H, M, st);
     });
+    if (e == hipSuccess)
+        e = timed(m, BH_K_NORM, [&] {
+            return launch_resid_norm(m->x, nullptr, 0, 0, nullptr, m->L[0].ln1, c.rms_eps, m->h, M, H, st);
+        });
     for (int l = 0; l < c.n_layers && e == hipSuccess; ++l) {
         LayerW& w = m->L[l];
-        e = timed(m, BH_K_NORM, [&] { return launch_rmsnorm(m->x, w.ln1, c.rms_eps, m->h, M, H, st); });
-        if (e != hipSuccess) break;
         GemvArgs a;
         a.W = w.qkv.q;
         a.S = w.qkv.s;
@@ -187,6 +194,7 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
         at.split_rows = split_rows;
         at.part_o = m->attn_part;
         at.part_ml = m->attn_part + (size_t)c.max_tokens * c.n_heads * m->max_splits * c.head_dim;
+        at.cnt = m->attn_cnt;
         e = timed(m, BH_K_ATTN, [&] { return launch_attention(at, st); });
         if (e != hipSuccess) break;
         GemvArgs o;
@@ -194,16 +202,19 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
         o.S = w.o.s;
         o.x = m->att;
         o.ldx = m->QD;
-        o.y = m->x;
-        o.ldy = H;
-        o.bias = c.o_bias ? w.bo : nullptr;
         o.N = H;
         o.n_pad = (int)w.o.n_pad;
         o.C = (int)w.o.chunks;
         o.batch = M;
-        e = timed(m, BH_K_GEMV_O, [&] { return launch_gemv(c.wfmt, EPI_RESID, o, st); });
+        o.part = m->gemv_part;
+        o.part_ld = m->part_ld;
+        o.ksw = part_splits((int)(w.o.n_pad / 64), (int)w.o.chunks);
+        e = timed(m, BH_K_GEMV_O, [&] { return launch_gemv(c.wfmt, EPI_PART, o, st); });
         if (e != hipSuccess) break;
-        e = timed(m, BH_K_NORM, [&] { return launch_rmsnorm(m->x, w.ln2, c.rms_eps, m->h, M, H, st); });
+        e = timed(m, BH_K_NORM, [&] {
+            return launch_resid_norm(m->x, m->gemv_part, o.ksw, m->part_ld, c.o_bias ? w.bo : nullptr, w.ln2,
+                                     c.rms_eps, m->h, M, H, st);
+        });
         if (e != hipSuccess) break;
         GemvArgs gu;
         gu.W = w.gate.q;
@@ -225,17 +236,21 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
         d.S = w.down.s;
         d.x = m->mm;
         d.ldx = I;
-        d.y = m->x;
-        d.ldy = H;
         d.N = H;
         d.n_pad = (int)w.down.n_pad;
         d.C = (int)w.down.chunks;
         d.batch = M;
-        e = timed(m, BH_K_GEMV_DOWN, [&] { return launch_gemv(c.wfmt, EPI_RESID, d, st); });
+        d.part = m->gemv_part;
+        d.part_ld = m->part_ld;
+        d.ksw = part_splits((int)(w.down.n_pad / 64), (int)w.down.chunks);
+        e = timed(m, BH_K_GEMV_DOWN, [&] { return launch_gemv(c.wfmt, EPI_PART, d, st); });
+        if (e != hipSuccess) break;
+        const float* next_w = l + 1 < c.n_layers ? m->L[l + 1].ln1 : m->norm;  // final norm after the last layer
+        e = timed(m, BH_K_NORM, [&] {
+            return launch_resid_norm(m->x, m->gemv_part, d.ksw, m->part_ld, nullptr, next_w, c.rms_eps, m->h, M, H, st);
+        });
     }
     if (e != hipSuccess || !logits) return e;
-    e = timed(m, BH_K_NORM, [&] { return launch_rmsnorm(m->x, m->norm, c.rms_eps, m->h, M, H, st); });
-    if (e != hipSuccess) return e;
     GemvArgs lm;
     lm.W = m->embed.q;
     lm.S = m->embed.s;
@@ -349,9 +364,8 @@ int bh_model_create(bh_ctx* ctx, const bh_model_config* cfg, bh_model** out) {
     if (c.n_layers <= 0 || c.hidden <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.ffn <= 0 || c.vocab <= 0 ||
         c.n_heads % c.n_kv_heads || c.max_seqs <= 0 || c.kv_rows <= 0 || c.max_tokens <= 0)
         return ctx->fail(BH_ERR_INVALID, "invalid model config");
-    if (c.head_dim != 64 && c.head_dim != 128)
-        return ctx->fail(BH_ERR_UNSUPPORTED, "head_dim must be 64 or 128");
-    if (c.n_heads / c.n_kv_heads > 8) return ctx->fail(BH_ERR_UNSUPPORTED, "at most 8 query heads per KV head");
+    if (!attn_supported(c.n_heads, c.n_kv_heads, c.head_dim))
+        return ctx->fail(BH_ERR_UNSUPPORTED, "head_dim must be 64 or 128 with 1, 2, 4, 7 or 8 query heads per KV head");
     if (c.head_fmt != BH_F32 && c.head_fmt != BH_Q4_G32)
         return ctx->fail(BH_ERR_UNSUPPORTED, "tied embedding format must be F32 or Q4_G32");
     if (c.wfmt < BH_F32 || c.wfmt > BH_Q4_G32) return ctx->fail(BH_ERR_INVALID, "unknown weight format");
@@ -362,6 +376,7 @@ int bh_model_create(bh_ctx* ctx, const bh_model_config* cfg, bh_model** out) {
     if (c.max_context > 0 && (c.sink_tokens < 0 || c.sink_tokens >= c.max_context))
         return ctx->fail(BH_ERR_INVALID, "sink_tokens must be below max_context");
     if (c.max_tokens > 4096) return ctx->fail(BH_ERR_UNSUPPORTED, "max_tokens above 4096");
+    if (c.hidden > 4096) return ctx->fail(BH_ERR_UNSUPPORTED, "hidden above 4096");
 
     std::lock_guard<std::mutex> g(ctx->mu);
     bh_model* m = new bh_model();
@@ -373,6 +388,7 @@ int bh_model_create(bh_ctx* ctx, const bh_model_config* cfg, bh_model** out) {
     m->L.resize(c.n_layers);
     m->max_pos = (int)std::max<int64_t>(65536, c.kv_rows + 1);
     m->tiles_lm = (int)(pad64(c.vocab) / 64);
+    m->part_ld = (int64_t)c.max_tokens * c.hidden;
     auto bail = [&](hipError_t e, const char* what) {
         int rc = ctx->hip_fail(e, what);
         bh_model_destroy(m);
@@ -401,6 +417,8 @@ int bh_model_create(bh_ctx* ctx, const bh_model_config* cfg, bh_model** out) {
         {(void**)&m->part_val, T * m->tiles_lm * 4},
         {(void**)&m->part_idx, T * m->tiles_lm * 4},
         {(void**)&m->attn_part, T * c.n_heads * m->max_splits * (c.head_dim + 2) * 4},
+        {(void**)&m->attn_cnt, T * c.n_kv_heads * 4},
+        {(void**)&m->gemv_part, (size_t)16 * T * c.hidden * 4},
         {(void**)&m->d_tok, T * 4},
         {(void**)&m->d_pos, T * 4},
         {(void**)&m->d_slot, T * 4},

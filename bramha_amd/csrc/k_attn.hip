@@ -7,12 +7,13 @@
 // Design: one workgroup per (query row, KV head, context split). The G = n_q/n_kv
 // query heads that share a KV head are processed together, so every K/V byte is
 // read once per workgroup instead of once per query head (the reference re-reads
-// each KV head's rows G times). Each wavefront takes 64-row tiles: in the score
-// phase lane t owns row t (16-byte loads of its K row, q broadcast from LDS); in
-// the value phase 8 (hd 64) or 4 (hd 128) rows are read per instruction with
-// 16-byte loads and the probabilities move between lanes with ds_bpermute. Splits
-// over long contexts write (m, l, o) partials that a second kernel merges with
-// log-sum-exp weights (flash-decoding).
+// each KV head's rows G times). Each wavefront takes 64-row tiles and requests the
+// tile's K rows (lane t owns row t, 16-byte loads) and V rows (8 rows per step for
+// hd 64, 16-byte loads) together before computing: scores use q broadcast from LDS,
+// probabilities move between lanes with ds_bpermute. G is a compile-time constant
+// so all per-head state stays in registers. Splits of long contexts publish
+// (m, l, o) partials; the last workgroup of a (row, KV head) to finish merges them
+// with log-sum-exp weights (flash-decoding) — no second kernel.
 #include "bh_internal.h"
 
 #include <hip/hip_fp16.h>
@@ -20,7 +21,7 @@
 namespace bh {
 namespace {
 
-constexpr int MAXG = 8;
+constexpr int MAX_SPLITS = 128;
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -34,34 +35,50 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 template <int KVF16>
-__device__ __forceinline__ void load8(const void* base, int64_t elem, float* f) {
-    if constexpr (KVF16) {
-        const uint4 u = *(const uint4*)((const __half*)base + elem);
-        const __half2* h2 = (const __half2*)&u;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float2 t = __half22float2(h2[i]);
-            f[2 * i] = t.x;
-            f[2 * i + 1] = t.y;
-        }
-    } else {
-        const float4 a = *(const float4*)((const float*)base + elem);
-        const float4 b = *(const float4*)((const float*)base + elem + 4);
-        f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
-        f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
-    }
+__device__ __forceinline__ uint4 load16(const void* base, int64_t elem) {
+    if constexpr (KVF16) return *(const uint4*)((const __half*)base + elem);
+    else return *(const uint4*)((const float*)base + elem);
 }
 
-template <int HD, int KVF16>
+// 8 consecutive elements starting at `elem`: one 16-byte load for fp16, two for f32.
+template <int KVF16>
+struct Row8 {
+    uint4 a, b;
+    __device__ __forceinline__ void load(const void* base, int64_t elem) {
+        a = load16<KVF16>(base, elem);
+        if constexpr (!KVF16) b = load16<KVF16>(base, elem + 4);
+    }
+    __device__ __forceinline__ void zero() {
+        a = make_uint4(0, 0, 0, 0);
+        b = a;
+    }
+    __device__ __forceinline__ void to_float(float* f) const {
+        if constexpr (KVF16) {
+            const __half2* h2 = (const __half2*)&a;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float2 t = __half22float2(h2[i]);
+                f[2 * i] = t.x;
+                f[2 * i + 1] = t.y;
+            }
+        } else {
+            f[0] = __uint_as_float(a.x); f[1] = __uint_as_float(a.y); f[2] = __uint_as_float(a.z); f[3] = __uint_as_float(a.w);
+            f[4] = __uint_as_float(b.x); f[5] = __uint_as_float(b.y); f[6] = __uint_as_float(b.z); f[7] = __uint_as_float(b.w);
+        }
+    }
+};
+
+template <int HD, int KVF16, int G>
 __global__ void __launch_bounds__(256) k_attn(const AttnArgs a) {
     constexpr int DL = HD / 8;   // lanes per row in the value phase
     constexpr int TS = 64 / DL;  // rows per value-phase step
-    __shared__ float q_s[MAXG][HD];
-    __shared__ float w_m[4][MAXG], w_l[4][MAXG];
-    __shared__ float w_o[4][MAXG][HD];
+    constexpr int NV = 64 / TS;  // value-phase steps per 64-row tile
+    __shared__ float q_s[G][HD];
+    __shared__ float w_m[4][G], w_l[4][G];
+    __shared__ float w_o[4][G][HD];
+    __shared__ int s_last;
 
     const int b = blockIdx.z, h = blockIdx.y, sp = blockIdx.x;
-    const int G = a.nq / a.nkv;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 
     int64_t off;
@@ -83,9 +100,9 @@ __global__ void __launch_bounds__(256) k_attn(const AttnArgs a) {
 
     const float scale = 1.0f / sqrtf((float)HD);
     const int64_t kv_base = ((int64_t)h * a.kv.kv_rows + off) * HD;
-    float m[MAXG], l[MAXG], o[MAXG][8];
+    float m[G], l[G], o[G][8];
 #pragma unroll
-    for (int g = 0; g < MAXG; ++g) {
+    for (int g = 0; g < G; ++g) {
         m[g] = -INFINITY;
         l[g] = 0.f;
 #pragma unroll
@@ -96,93 +113,97 @@ __global__ void __launch_bounds__(256) k_attn(const AttnArgs a) {
     for (int t0 = r0 + wave * 64; t0 < r1; t0 += 4 * 64) {
         const int t = t0 + lane;
         const bool valid = t < r1;
-        float s[MAXG];
+        // request the tile's K and V rows together
+        Row8<KVF16> kr[HD / 8], vr[NV];
 #pragma unroll
-        for (int g = 0; g < MAXG; ++g) s[g] = 0.f;
-        if (valid) {
-#pragma unroll
-            for (int dc = 0; dc < HD / 8; ++dc) {
-                float kf[8];
-                load8<KVF16>(a.kv.k, kv_base + (int64_t)t * HD + dc * 8, kf);
-#pragma unroll
-                for (int g = 0; g < MAXG; ++g) {
-                    if (g < G) {
-                        const float4 qa = *(const float4*)&q_s[g][dc * 8];
-                        const float4 qb = *(const float4*)&q_s[g][dc * 8 + 4];
-                        float acc = s[g];
-                        acc = fmaf(qa.x, kf[0], acc);
-                        acc = fmaf(qa.y, kf[1], acc);
-                        acc = fmaf(qa.z, kf[2], acc);
-                        acc = fmaf(qa.w, kf[3], acc);
-                        acc = fmaf(qb.x, kf[4], acc);
-                        acc = fmaf(qb.y, kf[5], acc);
-                        acc = fmaf(qb.z, kf[6], acc);
-                        acc = fmaf(qb.w, kf[7], acc);
-                        s[g] = acc;
-                    }
-                }
-            }
-        }
-        float pg[MAXG];
-#pragma unroll
-        for (int g = 0; g < MAXG; ++g) {
-            if (g < G) {
-                const float sc = valid ? s[g] * scale : -INFINITY;
-                const float mn = fmaxf(m[g], wave_max(sc));
-                const float alpha = m[g] == -INFINITY ? 0.f : expf(m[g] - mn);
-                const float p = valid ? expf(sc - mn) : 0.f;
-                l[g] = l[g] * alpha + wave_sum(p);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) o[g][e] *= alpha;
-                m[g] = mn;
-                pg[g] = p;
-            }
+        for (int dc = 0; dc < HD / 8; ++dc) {
+            if (valid) kr[dc].load(a.kv.k, kv_base + (int64_t)t * HD + dc * 8);
+            else kr[dc].zero();
         }
 #pragma unroll
-        for (int j = 0; j < 64 / TS; ++j) {
-            const int tl = j * TS + tsub;
-            const int t2 = t0 + tl;
+        for (int j = 0; j < NV; ++j) {
+            const int t2 = t0 + j * TS + tsub;
+            if (t2 < r1) vr[j].load(a.kv.v, kv_base + (int64_t)t2 * HD + dl * 8);
+            else vr[j].zero();
+        }
+        float s[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) s[g] = 0.f;
+#pragma unroll
+        for (int dc = 0; dc < HD / 8; ++dc) {
+            float kf[8];
+            kr[dc].to_float(kf);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float4 qa = *(const float4*)&q_s[g][dc * 8];
+                const float4 qb = *(const float4*)&q_s[g][dc * 8 + 4];
+                float acc = s[g];
+                acc = fmaf(qa.x, kf[0], acc);
+                acc = fmaf(qa.y, kf[1], acc);
+                acc = fmaf(qa.z, kf[2], acc);
+                acc = fmaf(qa.w, kf[3], acc);
+                acc = fmaf(qb.x, kf[4], acc);
+                acc = fmaf(qb.y, kf[5], acc);
+                acc = fmaf(qb.z, kf[6], acc);
+                acc = fmaf(qb.w, kf[7], acc);
+                s[g] = acc;
+            }
+            // keep the q reads of later chunks from being hoisted into registers
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        float pg[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float sc = valid ? s[g] * scale : -INFINITY;
+            const float mn = fmaxf(m[g], wave_max(sc));
+            const float alpha = m[g] == -INFINITY ? 0.f : expf(m[g] - mn);
+            const float p = valid ? expf(sc - mn) : 0.f;
+            l[g] = l[g] * alpha + wave_sum(p);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[g][e] *= alpha;
+            m[g] = mn;
+            pg[g] = p;
+        }
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
             float vf[8];
-            if (t2 < r1) {
-                load8<KVF16>(a.kv.v, kv_base + (int64_t)t2 * HD + dl * 8, vf);
-            } else {
+            vr[j].to_float(vf);
+            const int tl = j * TS + tsub;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) vf[e] = 0.f;
-            }
+            for (int g = 0; g < G; ++g) {
+                const float pp = __shfl(pg[g], tl);
 #pragma unroll
-            for (int g = 0; g < MAXG; ++g) {
-                if (g < G) {
-                    const float pp = __shfl(pg[g], tl);
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) o[g][e] = fmaf(pp, vf[e], o[g][e]);
-                }
+                for (int e = 0; e < 8; ++e) o[g][e] = fmaf(pp, vf[e], o[g][e]);
             }
         }
     }
     // sum the value accumulators of the lanes that share a column slice
 #pragma unroll
-    for (int g = 0; g < MAXG; ++g) {
-        if (g < G) {
+    for (int g = 0; g < G; ++g) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                float v = o[g][e];
+        for (int e = 0; e < 8; ++e) {
+            float v = o[g][e];
 #pragma unroll
-                for (int x = DL; x < 64; x <<= 1) v += __shfl_xor(v, x);
-                o[g][e] = v;
-            }
+            for (int x = DL; x < 64; x <<= 1) v += __shfl_xor(v, x);
+            o[g][e] = v;
         }
     }
-    if (lane == 0)
+    if (lane == 0) {
+#pragma unroll
         for (int g = 0; g < G; ++g) {
             w_m[wave][g] = m[g];
             w_l[wave][g] = l[g];
         }
-    if (tsub == 0)
+    }
+    if (tsub == 0) {
+#pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
             for (int e = 0; e < 8; ++e) w_o[wave][g][dl * 8 + e] = o[g][e];
+    }
     __syncthreads();
 
+    const int64_t hq0 = (int64_t)b * a.nq + h * G;
     for (int i = threadIdx.x; i < G * HD; i += blockDim.x) {
         const int g = i / HD, d = i % HD;
         float M = -INFINITY;
@@ -193,70 +214,102 @@ __global__ void __launch_bounds__(256) k_attn(const AttnArgs a) {
             L += w_l[w][g] * f;
             O += w_o[w][g][d] * f;
         }
-        const int64_t hq = (int64_t)b * a.nq + h * G + g;
         if (a.splits == 1) {
-            a.out[hq * HD + d] = O * (1.0f / L);
+            a.out[(hq0 + g) * HD + d] = O * (1.0f / L);
         } else {
-            a.part_o[(hq * a.splits + sp) * HD + d] = O;
+            a.part_o[((hq0 + g) * a.splits + sp) * HD + d] = O;
             if (d == 0) {
-                a.part_ml[(hq * a.splits + sp) * 2] = M;
-                a.part_ml[(hq * a.splits + sp) * 2 + 1] = L;
+                a.part_ml[((hq0 + g) * a.splits + sp) * 2] = M;
+                a.part_ml[((hq0 + g) * a.splits + sp) * 2 + 1] = L;
             }
         }
     }
+    if (a.splits == 1) return;
+
+    // ---- the last workgroup of this (row, KV head) merges the splits ----
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) s_last = atomicAdd(&a.cnt[b * a.nkv + h], 1) == a.splits - 1;
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    __shared__ float f_s[G][MAX_SPLITS];
+    __shared__ float L_s[G];
+    const int S = a.splits;
+    for (int i = threadIdx.x; i < G * S; i += blockDim.x) {
+        const int g = i / S, s2 = i % S;
+        f_s[g][s2] = a.part_ml[((hq0 + g) * S + s2) * 2];
+    }
+    __syncthreads();
+    if (threadIdx.x < G) {
+        const int g = threadIdx.x;
+        float M = -INFINITY;
+        for (int s2 = 0; s2 < S; ++s2) M = fmaxf(M, f_s[g][s2]);
+        float L = 0.f;
+        for (int s2 = 0; s2 < S; ++s2) {
+            const float ms = f_s[g][s2];
+            const float f = ms == -INFINITY ? 0.f : expf(ms - M);
+            L += a.part_ml[((hq0 + g) * S + s2) * 2 + 1] * f;
+            f_s[g][s2] = f;
+        }
+        L_s[g] = L;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < G * HD; i += blockDim.x) {
+        const int g = i / HD, d = i % HD;
+        float O = 0.f;
+        for (int s2 = 0; s2 < S; ++s2) O = fmaf(f_s[g][s2], a.part_o[((hq0 + g) * S + s2) * HD + d], O);
+        a.out[(hq0 + g) * HD + d] = O * (1.0f / L_s[g]);
+    }
+    if (threadIdx.x == 0) a.cnt[b * a.nkv + h] = 0;  // ready for the next launch
 }
 
-// Log-sum-exp merge of the context splits.
-__global__ void k_attn_combine(const AttnArgs a) {
-    const int hq = blockIdx.x, b = blockIdx.y;
-    const int64_t base = ((int64_t)b * a.nq + hq) * a.splits;
-    float M = -INFINITY;
-    for (int s = 0; s < a.splits; ++s) M = fmaxf(M, a.part_ml[(base + s) * 2]);
-    for (int d = threadIdx.x; d < a.hd; d += blockDim.x) {
-        float L = 0.f, O = 0.f;
-        for (int s = 0; s < a.splits; ++s) {
-            const float ms = a.part_ml[(base + s) * 2];
-            const float f = ms == -INFINITY ? 0.f : expf(ms - M);
-            L += a.part_ml[(base + s) * 2 + 1] * f;
-            O += a.part_o[(base + s) * a.hd + d] * f;
-        }
-        a.out[((int64_t)b * a.nq + hq) * a.hd + d] = O * (1.0f / L);
-    }
+template <int HD, int KVF16, int G>
+hipError_t launch_t(const AttnArgs& a, hipStream_t st) {
+    hipLaunchKernelGGL((k_attn<HD, KVF16, G>), dim3(a.splits, a.nkv, a.batch), dim3(256), 0, st, a);
+    return hipGetLastError();
 }
 
 template <int HD, int KVF16>
-hipError_t launch_t(const AttnArgs& a, hipStream_t st) {
-    hipLaunchKernelGGL((k_attn<HD, KVF16>), dim3(a.splits, a.nkv, a.batch), dim3(256), 0, st, a);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess || a.splits == 1) return e;
-    hipLaunchKernelGGL(k_attn_combine, dim3(a.nq, a.batch), dim3(HD), 0, st, a);
-    return hipGetLastError();
+hipError_t launch_g(const AttnArgs& a, hipStream_t st) {
+    switch (a.nq / a.nkv) {
+        case 1: return launch_t<HD, KVF16, 1>(a, st);
+        case 2: return launch_t<HD, KVF16, 2>(a, st);
+        case 4: return launch_t<HD, KVF16, 4>(a, st);
+        case 7: return launch_t<HD, KVF16, 7>(a, st);
+        case 8: return launch_t<HD, KVF16, 8>(a, st);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace
 
+// Context split: 256 rows per workgroup (one 64-row tile per wave); 64 when that leaves
+// fewer than 256 workgroups; at most 128 splits (longer splits loop over tiles).
 void attn_plan(int max_len, int batch, int nkv, int* splits, int* split_rows) {
-    if (max_len <= 256) {
-        *splits = 1;
-        *split_rows = std::max(64, (max_len + 63) / 64 * 64);
-        return;
-    }
+    max_len = std::max(max_len, 1);
     int rows = 256;
-    while (rows > 64 && (int64_t)((max_len + rows - 1) / rows) * nkv * batch < 512) rows /= 2;
+    if ((int64_t)((max_len + 255) / 256) * nkv * batch < 256) rows = 64;
     int s = (max_len + rows - 1) / rows;
-    if (s > 128) {
-        rows = ((max_len + 127) / 128 + 63) / 64 * 64;
+    if (s > MAX_SPLITS) {
+        rows = ((max_len + MAX_SPLITS - 1) / MAX_SPLITS + 255) / 256 * 256;
         s = (max_len + rows - 1) / rows;
     }
     *splits = s;
     *split_rows = rows;
 }
 
+bool attn_supported(int nq, int nkv, int hd) {
+    if (nkv <= 0 || nq % nkv) return false;
+    const int g = nq / nkv;
+    return (hd == 64 || hd == 128) && (g == 1 || g == 2 || g == 4 || g == 7 || g == 8);
+}
+
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
-    if (a.nq % a.nkv != 0 || a.nq / a.nkv > MAXG) return hipErrorInvalidValue;
-    if (a.hd == 64) return a.kv.kv_f16 ? launch_t<64, 1>(a, st) : launch_t<64, 0>(a, st);
-    if (a.hd == 128) return a.kv.kv_f16 ? launch_t<128, 1>(a, st) : launch_t<128, 0>(a, st);
-    return hipErrorInvalidValue;
+    if (!attn_supported(a.nq, a.nkv, a.hd) || a.splits > MAX_SPLITS || (a.splits > 1 && !a.cnt))
+        return hipErrorInvalidValue;
+    if (a.hd == 64) return a.kv.kv_f16 ? launch_g<64, 1>(a, st) : launch_g<64, 0>(a, st);
+    return a.kv.kv_f16 ? launch_g<128, 1>(a, st) : launch_g<128, 0>(a, st);
 }
 
 }  // namespace bh

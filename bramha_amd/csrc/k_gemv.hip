@@ -9,14 +9,17 @@
 // streams 1 KiB of contiguous weight bytes per chunk step with one
 // global_load_dwordx4 per lane. The activations of a chunk are identical for all
 // 64 lanes, so they arrive through scalar loads (s_load_dwordx16) and enter the
-// FMAs as SGPR operands: no LDS traffic and no cross-lane reduction in the main
-// loop. Nibbles are decoded as signed int4 (q ^ 8 == q - 8 in two's complement)
-// shifted into the top of a byte and converted with the SDWA sign-extending
-// byte convert: one VALU op per element plus three bit ops per 8 elements; the
-// resulting factor 16 is folded into the scale. Waves of a workgroup split the
-// K range; their partial sums are combined in LDS in a fixed order, so results
-// are deterministic. Epilogues fuse the bias, residual add, SiLU gate, RoPE +
-// KV-cache append, and LM-head repetition penalty + per-tile argmax.
+// FMAs as SGPR operands: no LDS traffic and no cross-lane reduction in the main loop.
+// Nibbles are decoded as signed int4 (q ^ 8 == q - 8 in two's complement) shifted
+// into the top of a byte and converted with the SDWA sign-extending byte convert:
+// one VALU op per element plus three bit ops per 8 elements; the factor 16 is
+// folded into the scale. The chunk loop is software-pipelined (the next batch of
+// chunks is in flight while the current one is converted). Waves of a workgroup split
+// K and combine in LDS in a fixed order; matrices with few row tiles also split K
+// across workgroups, which store partial sums that the next kernel (residual-reduce +
+// RMSNorm) adds in a fixed order, so results are deterministic without atomics.
+// Epilogues fuse the bias, residual add, SiLU gate, RoPE + KV-cache append, and the
+// LM-head repetition penalty + per-tile argmax.
 #include "bh_internal.h"
 
 #include <hip/hip_fp16.h>
@@ -103,7 +106,8 @@ __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
     constexpr int E = Fmt<FMT>::E;
     constexpr int NACC = EPI == EPI_SILU ? 2 : 1;
     constexpr int ROWS = 64 * RW;
-    constexpr int U = FMT == BH_F32 ? 8 : 4;  // chunks in flight per lane
+    constexpr int U = NACC == 2 ? 2 : 4;  // chunks per pipeline stage (x2 stages in flight)
+    constexpr int TOT = NACC * B * ROWS;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -111,16 +115,17 @@ __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
     const int ksplit = nwaves / RW;
     const int rw = wave % RW, kw = wave / RW;
     const int r = rw * 64 + lane;
-    const int64_t n = (int64_t)blockIdx.x * ROWS + r;
-    const int per = (a.C + ksplit - 1) / ksplit;
-    const int c0 = kw * per;
-    const int c1 = min(a.C, c0 + per);
-
-    float acc[NACC][B];
-#pragma unroll
-    for (int j = 0; j < NACC; ++j)
-#pragma unroll
-        for (int b = 0; b < B; ++b) acc[j][b] = 0.f;
+    const int ksw = EPI == EPI_PART ? a.ksw : 1;
+    const int tiles = gridDim.x / ksw;
+    const int tile = blockIdx.x % tiles, kws = blockIdx.x / tiles;
+    const int64_t n = (int64_t)tile * ROWS + r;
+    // this workgroup's chunk range, then this wave's share of it
+    const int per_wg = (a.C + ksw - 1) / ksw;
+    const int wc0 = kws * per_wg, wc1 = min(a.C, wc0 + per_wg);
+    const int per = (max(wc1 - wc0, 0) + ksplit - 1) / ksplit;
+    const int c0 = wc0 + kw * per;
+    const int c1 = min(wc1, c0 + per);
+    const bool row_ok = n < a.n_pad;
 
     const uint4* Wp[NACC];
     const __half* Sp[NACC];
@@ -131,46 +136,59 @@ __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
         Sp[1] = (const __half*)a.S2 + n;
     }
 
-    if (n < a.n_pad) {
-        for (int c = c0; c < c1; c += U) {
-            uint4 q[NACC][U];
-            float s[NACC][U];
+    uint4 q0[NACC][U], q1[NACC][U];
+    float s0[NACC][U], s1[NACC][U];
+    auto fetch = [&](int c, uint4 (&q)[NACC][U], float (&s)[NACC][U]) {
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                if (c + u < c1) {
+        for (int u = 0; u < U; ++u) {
+            if (row_ok && c + u < c1) {
 #pragma unroll
-                    for (int j = 0; j < NACC; ++j) {
-                        q[j][u] = Wp[j][(int64_t)(c + u) * a.n_pad];
-                        if constexpr (FMT == BH_Q4_G32)
-                            s[j][u] = __half2float(Sp[j][(int64_t)(c + u) * a.n_pad]) * 0.0625f;
-                    }
+                for (int j = 0; j < NACC; ++j) {
+                    q[j][u] = Wp[j][(int64_t)(c + u) * a.n_pad];
+                    if constexpr (FMT == BH_Q4_G32) s[j][u] = __half2float(Sp[j][(int64_t)(c + u) * a.n_pad]);
                 }
             }
+        }
+    };
+    fetch(c0, q0, s0);
+
+    float acc[NACC][B];
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                if (c + u < c1) {
-                    const int kb = (c + u) * E;
+    for (int j = 0; j < NACC; ++j)
 #pragma unroll
-                    for (int j = 0; j < NACC; ++j) {
-                        float v[E];
-                        decode<FMT>(q[j][u], v);
+        for (int b = 0; b < B; ++b) acc[j][b] = 0.f;
+
+    auto consume = [&](int c, const uint4 (&q)[NACC][U], const float (&s)[NACC][U]) {
 #pragma unroll
-                        for (int b = 0; b < B; ++b) {
-                            const float* xb = a.x + (int64_t)b * a.ldx + kb;
-                            float p = 0.f;
+        for (int u = 0; u < U; ++u) {
+            if (row_ok && c + u < c1) {
+                const int kb = (c + u) * E;
 #pragma unroll
-                            for (int e = 0; e < E; ++e) p = fmaf(xb[e], v[e], p);
-                            if constexpr (FMT == BH_Q4_G32) acc[j][b] = fmaf(p, s[j][u], acc[j][b]);
-                            else acc[j][b] += p;
-                        }
+                for (int j = 0; j < NACC; ++j) {
+                    float v[E];
+                    decode<FMT>(q[j][u], v);
+#pragma unroll
+                    for (int b = 0; b < B; ++b) {
+                        const float* xb = a.x + (int64_t)b * a.ldx + kb;
+                        float p = 0.f;
+#pragma unroll
+                        for (int e = 0; e < E; ++e) p = fmaf(xb[e], v[e], p);
+                        if constexpr (FMT == BH_Q4_G32) acc[j][b] = fmaf(p, s[j][u] * 0.0625f, acc[j][b]);
+                        else acc[j][b] += p;
                     }
                 }
             }
         }
+    };
+    for (int c = c0; c < c1; c += 2 * U) {
+        fetch(c + U, q1, s1);
+        consume(c, q0, s0);
+        if (c + U >= c1) break;
+        fetch(c + 2 * U, q0, s0);
+        consume(c + U, q1, s1);
     }
 
     // ---- combine the K-split partial sums in a fixed order ----
-    constexpr int TOT = NACC * B * ROWS;
 #pragma unroll
     for (int j = 0; j < NACC; ++j)
 #pragma unroll
@@ -182,10 +200,19 @@ __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
         smem[i] = sum;
     }
     __syncthreads();
-    const float* fin = smem;
-    const int64_t row0 = (int64_t)blockIdx.x * ROWS;
+    const int64_t row0 = (int64_t)tile * ROWS;
 
-    if constexpr (EPI == EPI_STORE || EPI == EPI_RESID) {
+    const float* fin = smem;
+
+    if constexpr (EPI == EPI_PART) {
+        float* part = a.part + (int64_t)kws * a.part_ld;
+        for (int i = threadIdx.x; i < B * ROWS; i += blockDim.x) {
+            const int b = i / ROWS, rr = i % ROWS;
+            const int64_t nn = row0 + rr;
+            if (nn >= a.N || b >= a.batch) continue;
+            part[(int64_t)b * a.N + nn] = fin[i] * row_scale<FMT>(a.S, nn);
+        }
+    } else if constexpr (EPI == EPI_STORE || EPI == EPI_RESID) {
         for (int i = threadIdx.x; i < B * ROWS; i += blockDim.x) {
             const int b = i / ROWS, rr = i % ROWS;
             const int64_t nn = row0 + rr;
@@ -250,7 +277,6 @@ __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
             smem[TOT + i] = pv;
         }
         __syncthreads();
-        const int tiles = gridDim.x;
         for (int b = wave; b < B; b += nwaves) {
             if (b >= a.batch) continue;
             float v = smem[TOT + b * ROWS + lane];
@@ -262,66 +288,80 @@ __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
                 argmax_combine(v, idx, ov, oi);
             }
             if (lane == 0) {
-                a.part_val[(int64_t)b * tiles + blockIdx.x] = v;
-                a.part_idx[(int64_t)b * tiles + blockIdx.x] = idx;
+                a.part_val[(int64_t)b * tiles + tile] = v;
+                a.part_idx[(int64_t)b * tiles + tile] = idx;
             }
         }
     }
 }
 
 template <int FMT, int B, int EPI, int RW>
-hipError_t launch_one(const GemvArgs& a, int ksplit, hipStream_t st) {
+hipError_t launch_one(const GemvArgs& a, int ksplit, int ksw, hipStream_t st) {
     constexpr int NACC = EPI == EPI_SILU ? 2 : 1;
     constexpr int ROWS = 64 * RW;
     const int tiles = (a.n_pad + ROWS - 1) / ROWS;
     size_t shm = (size_t)ksplit * NACC * B * ROWS * sizeof(float);
-    if (EPI == EPI_LMHEAD) shm += (size_t)B * ROWS * sizeof(float);
-    hipLaunchKernelGGL((k_gemv<FMT, B, EPI, RW>), dim3(tiles), dim3(64 * RW * ksplit), shm, st, a);
+    if (EPI == EPI_LMHEAD) shm = std::max(shm, (size_t)(NACC * B * ROWS + B * ROWS) * sizeof(float));
+    hipLaunchKernelGGL((k_gemv<FMT, B, EPI, RW>), dim3(tiles * ksw), dim3(64 * RW * ksplit), shm, st, a);
     return hipGetLastError();
 }
 
 template <int FMT, int EPI, int RW>
-hipError_t launch_b(const GemvArgs& a, int B, int ksplit, hipStream_t st) {
+hipError_t launch_b(const GemvArgs& a, int B, int ksplit, int ksw, hipStream_t st) {
     switch (B) {
-        case 1: return launch_one<FMT, 1, EPI, RW>(a, ksplit, st);
-        case 2: return launch_one<FMT, 2, EPI, RW>(a, ksplit, st);
-        case 4: return launch_one<FMT, 4, EPI, RW>(a, ksplit, st);
-        default: return launch_one<FMT, 8, EPI, RW>(a, ksplit, st);
+        case 1: return launch_one<FMT, 1, EPI, RW>(a, ksplit, ksw, st);
+        case 2: return launch_one<FMT, 2, EPI, RW>(a, ksplit, ksw, st);
+        case 4: return launch_one<FMT, 4, EPI, RW>(a, ksplit, ksw, st);
+        default: return launch_one<FMT, 8, EPI, RW>(a, ksplit, ksw, st);
     }
 }
 
 template <int FMT>
-hipError_t launch_fmt(int epi, const GemvArgs& a, int B, int rw, int ksplit, hipStream_t st) {
+hipError_t launch_fmt(int epi, const GemvArgs& a, int B, int rw, int ksplit, int ksw, hipStream_t st) {
     switch (epi) {
-        case EPI_STORE: return launch_b<FMT, EPI_STORE, 1>(a, B, ksplit, st);
-        case EPI_RESID: return launch_b<FMT, EPI_RESID, 1>(a, B, ksplit, st);
-        case EPI_SILU: return launch_b<FMT, EPI_SILU, 1>(a, B, ksplit, st);
+        case EPI_STORE: return launch_b<FMT, EPI_STORE, 1>(a, B, ksplit, ksw, st);
+        case EPI_RESID: return launch_b<FMT, EPI_RESID, 1>(a, B, ksplit, ksw, st);
+        case EPI_SILU: return launch_b<FMT, EPI_SILU, 1>(a, B, ksplit, ksw, st);
+        case EPI_PART: return launch_b<FMT, EPI_PART, 1>(a, B, ksplit, ksw, st);
         case EPI_QKV:
-            return rw == 2 ? launch_b<FMT, EPI_QKV, 2>(a, B, ksplit, st) : launch_b<FMT, EPI_QKV, 1>(a, B, ksplit, st);
+            return rw == 2 ? launch_b<FMT, EPI_QKV, 2>(a, B, ksplit, ksw, st)
+                           : launch_b<FMT, EPI_QKV, 1>(a, B, ksplit, ksw, st);
         default:
-            if constexpr (FMT == BH_F32 || FMT == BH_Q4_G32) return launch_b<FMT, EPI_LMHEAD, 1>(a, B, ksplit, st);
+            if constexpr (FMT == BH_F32 || FMT == BH_Q4_G32) return launch_b<FMT, EPI_LMHEAD, 1>(a, B, ksplit, ksw, st);
             return hipErrorInvalidValue;
     }
 }
 
 }  // namespace
 
-// Splits the batch into passes of at most 8 rows and sizes the K split so that
-// small matrices still occupy a few waves per CU.
+// Waves per workgroup along K: aim for ~8 waves per CU and >= 2 chunks per wave.
+static int waves_per_tile(int tiles, int rw, int C, int nacc, int B) {
+    int ks = (2048 + tiles * rw - 1) / (tiles * rw);
+    ks = std::max(1, std::min({ks, 16 / rw, std::max(1, C / 2)}));
+    while (ks > 1 && (size_t)ks * nacc * B * 64 * rw * 4 > 60 * 1024) --ks;
+    return ks;
+}
+
+// Workgroups per row tile for EPI_PART: about one workgroup per CU (256) with at least
+// two chunks each, at most 16 splits.
+int part_splits(int tiles, int C) {
+    const int ksw = 256 / std::max(tiles, 1);
+    return std::max(1, std::min({ksw, 16, std::max(1, C / 2)}));
+}
+
+// Splits the batch into passes of at most 8 rows; EPI_PART uses a.ksw workgroups per tile.
 hipError_t launch_gemv(int fmt, int epi, const GemvArgs& a0, hipStream_t st) {
     const int rw = (epi == EPI_QKV && a0.hd > 64) ? a0.hd / 64 : 1;
     if (rw > 2) return hipErrorInvalidValue;
+    if (epi == EPI_PART && (!a0.part || a0.ksw < 1)) return hipErrorInvalidValue;
     const int nacc = epi == EPI_SILU ? 2 : 1;
     const int tiles = (a0.n_pad + 64 * rw - 1) / (64 * rw);
+    const int ksw = epi == EPI_PART ? a0.ksw : 1;
     int b0 = 0;
     while (b0 < a0.batch) {
         const int rem = a0.batch - b0;
         const int B = rem >= 8 ? 8 : (rem >= 4 ? 4 : (rem >= 2 ? 2 : 1));
-        int ks = (2048 + tiles * rw - 1) / (tiles * rw);  // target ~2048 waves
-        ks = std::min(ks, 16 / rw);
-        ks = std::min(ks, std::max(1, a0.C / 2));
-        while (ks > 1 && (size_t)ks * nacc * B * 64 * rw * 4 > 60 * 1024) --ks;
-        if (ks < 1) ks = 1;
+        int ks = waves_per_tile(tiles * ksw, rw, (a0.C + ksw - 1) / ksw, nacc, B);
         GemvArgs a = a0;
         a.batch = B;
         a.x = a0.x + (int64_t)b0 * a0.ldx;
@@ -330,12 +370,13 @@ hipError_t launch_gemv(int fmt, int epi, const GemvArgs& a0, hipStream_t st) {
         if (a0.slot) a.slot = a0.slot + b0;
         if (a0.part_val) a.part_val = a0.part_val + (int64_t)b0 * tiles;
         if (a0.part_idx) a.part_idx = a0.part_idx + (int64_t)b0 * tiles;
+        if (a0.part) a.part = a0.part + (int64_t)b0 * a0.N;
         hipError_t e;
         switch (fmt) {
-            case BH_F32: e = launch_fmt<BH_F32>(epi, a, B, rw, ks, st); break;
-            case BH_Q8_ROW: e = launch_fmt<BH_Q8_ROW>(epi, a, B, rw, ks, st); break;
-            case BH_Q4_ROW: e = launch_fmt<BH_Q4_ROW>(epi, a, B, rw, ks, st); break;
-            case BH_Q4_G32: e = launch_fmt<BH_Q4_G32>(epi, a, B, rw, ks, st); break;
+            case BH_F32: e = launch_fmt<BH_F32>(epi, a, B, rw, ks, ksw, st); break;
+            case BH_Q8_ROW: e = launch_fmt<BH_Q8_ROW>(epi, a, B, rw, ks, ksw, st); break;
+            case BH_Q4_ROW: e = launch_fmt<BH_Q4_ROW>(epi, a, B, rw, ks, ksw, st); break;
+            case BH_Q4_G32: e = launch_fmt<BH_Q4_G32>(epi, a, B, rw, ks, ksw, st); break;
             default: return hipErrorInvalidValue;
         }
         if (e != hipSuccess) return e;

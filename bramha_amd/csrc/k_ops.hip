@@ -32,6 +32,54 @@ __global__ void __launch_bounds__(256) k_rmsnorm(const float* __restrict__ x, co
     for (int i = threadIdx.x; i < n; i += blockDim.x) orow[i] = xr[i] * scale * w[i];
 }
 
+// The residual add of the O / down projection (cpu_engine.rs:2937-2939, 2966-2968)
+// followed by the next RMSNorm (rms_norm_into, :1292-1302), one workgroup per row:
+// o = sum of the projection's split-K partial sums in split order (+ bias), x += o,
+// h = x * (1/sqrt(mean(x^2) + eps)) * w. Holds up to 16 elements per thread (n <= 4096).
+__global__ void __launch_bounds__(256) k_resid_norm(float* __restrict__ x, const float* __restrict__ part,
+                                                    int splits, int64_t part_ld, const float* __restrict__ bias,
+                                                    const float* __restrict__ w, float eps, float* __restrict__ h,
+                                                    int n) {
+    __shared__ float red[16];
+    constexpr int MAXJ = 16;
+    const int b = blockIdx.x;
+    float* xr = x + (int64_t)b * n;
+    float v[MAXJ];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < MAXJ; ++j) {
+        const int i = threadIdx.x + j * blockDim.x;
+        v[j] = 0.f;
+        if (i < n) {
+            float t = xr[i];
+            if (splits > 0) {
+                // all (up to 16) partial loads in flight at once: the index is clamped so
+                // every load is in bounds, the add is masked past `splits`
+                const float* pp = part + (int64_t)b * n + i;
+                float pv[16];
+#pragma unroll
+                for (int s = 0; s < 16; ++s) pv[s] = pp[(int64_t)min(s, splits - 1) * part_ld];
+                float o = 0.f;
+#pragma unroll
+                for (int s = 0; s < 16; ++s) o += s < splits ? pv[s] : 0.f;
+                if (bias) o += bias[i];
+                t = t + o;
+                xr[i] = t;
+            }
+            v[j] = t;
+            ss += t * t;
+        }
+    }
+    ss = block_sum(ss, red);
+    const float scale = 1.0f / sqrtf(ss / (float)n + eps);
+    float* hr = h + (int64_t)b * n;
+#pragma unroll
+    for (int j = 0; j < MAXJ; ++j) {
+        const int i = threadIdx.x + j * blockDim.x;
+        if (i < n) hr[i] = v[j] * scale * w[i];
+    }
+}
+
 // apply_rope_cpu (cpu_engine.rs:1682-1699) with a host-computed (cos, sin) table.
 __global__ void k_rope(float* __restrict__ v, const int32_t* __restrict__ pos, const float2* __restrict__ tab,
                        int n_heads, int hd) {
@@ -180,6 +228,13 @@ __global__ void k_step_counter(int32_t* ctr, int reset) { ctr[0] = reset ? 0 : c
 
 hipError_t launch_rmsnorm(const float* x, const float* w, float eps, float* out, int rows, int n, hipStream_t st) {
     hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(256), 0, st, x, w, eps, out, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_resid_norm(float* x, const float* part, int splits, int64_t part_ld, const float* bias,
+                             const float* w, float eps, float* h, int rows, int n, hipStream_t st) {
+    if (n > 16 * 256 || splits > 16) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_resid_norm, dim3(rows), dim3(256), 0, st, x, part, splits, part_ld, bias, w, eps, h, n);
     return hipGetLastError();
 }
 

@@ -1,24 +1,53 @@
-"""Device-pointer operators of the C ABI (bh_gemv, bh_dequant, bh_rmsnorm, bh_rope,
-bh_silu_mul, bh_attn_decode). Arguments are torch tensors on the device (torch is
-used only for device memory and streams) and work is ordered on the current torch
-stream."""
+"""Device buffers and single device operators of the C ABI (bh_dev_*, bh_gemv,
+bh_dequant, bh_rmsnorm, bh_rope, bh_silu_mul, bh_attn_decode).
+
+Buffers are allocated through the library itself, so no other GPU runtime shares the
+process; all work is ordered on the context's stream and every copy back to the host
+waits for it."""
 import ctypes
 
 import numpy as np
 
-from . import _lib
 from ._lib import check, lib, ptr
 
 
-def _stream():
-    import torch
+class DeviceArray:
+    """A device buffer with a numpy shape and dtype."""
 
-    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    def __init__(self, plane, shape, dtype):
+        self.plane = plane
+        self.shape = tuple(int(s) for s in np.atleast_1d(shape))
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape)) * self.dtype.itemsize
+        h = ctypes.c_void_p()
+        check(lib.bh_dev_alloc(plane.ctx, self.nbytes, ctypes.byref(h)), plane.ctx)
+        self.ptr = h.value
 
+    @classmethod
+    def from_numpy(cls, plane, a):
+        a = np.ascontiguousarray(a)
+        d = cls(plane, a.shape, a.dtype)
+        check(lib.bh_memcpy_h2d(plane.ctx, d.ptr, ptr(a), a.nbytes), plane.ctx)
+        return d
 
-def _host_bytes(a):
-    a = np.ascontiguousarray(a)
-    return a, a.nbytes
+    def numpy(self):
+        out = np.empty(self.shape, self.dtype)
+        check(lib.bh_memcpy_d2h(self.plane.ctx, ptr(out), self.ptr, self.nbytes), self.plane.ctx)
+        return out
+
+    def data_ptr(self):
+        return self.ptr
+
+    def free(self):
+        if self.ptr and self.plane.ctx:
+            lib.bh_dev_free(self.plane.ctx, self.ptr)
+        self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
 
 
 class DeviceWeight:
@@ -27,10 +56,11 @@ class DeviceWeight:
     def __init__(self, plane, fmt, n, k, q, scales=None):
         self.plane = plane
         self.fmt, self.n, self.k = fmt, n, k
-        q, qb = _host_bytes(q)
-        s, sb = (None, 0) if scales is None else _host_bytes(scales)
+        q = np.ascontiguousarray(q)
+        s = None if scales is None else np.ascontiguousarray(scales)
         h = ctypes.c_void_p()
-        check(lib.bh_weight_upload(plane.ctx, fmt, n, k, ptr(q), qb, ptr(s), sb, ctypes.byref(h)), plane.ctx)
+        check(lib.bh_weight_upload(plane.ctx, fmt, n, k, ptr(q), q.nbytes, ptr(s), 0 if s is None else s.nbytes,
+                                   ctypes.byref(h)), plane.ctx)
         self.handle = h.value
 
     def free(self):
@@ -44,55 +74,47 @@ class DeviceWeight:
         except Exception:
             pass
 
-    def gemv(self, x, y=None):
-        import torch
-
-        assert x.is_cuda and x.dtype == torch.float32 and x.is_contiguous() and x.shape[-1] == self.k
-        batch = x.numel() // self.k
-        if y is None:
-            y = torch.empty(batch, self.n, device=x.device, dtype=torch.float32)
-        check(lib.bh_gemv(self.plane.ctx, self.handle, ptr(x), ptr(y), batch, _stream()), self.plane.ctx)
+    def gemv(self, x):
+        """x: DeviceArray f32 [batch, k] -> DeviceArray f32 [batch, n]."""
+        assert x.dtype == np.float32 and x.shape[-1] == self.k
+        batch = int(np.prod(x.shape)) // self.k
+        y = DeviceArray(self.plane, (batch, self.n), np.float32)
+        check(lib.bh_gemv(self.plane.ctx, self.handle, x.ptr, y.ptr, batch, None), self.plane.ctx)
         return y
 
     def dequant(self):
-        import torch
-
-        out = torch.empty(self.n, self.k, device="cuda", dtype=torch.float32)
-        check(lib.bh_dequant(self.plane.ctx, self.handle, ptr(out), _stream()), self.plane.ctx)
+        out = DeviceArray(self.plane, (self.n, self.k), np.float32)
+        check(lib.bh_dequant(self.plane.ctx, self.handle, out.ptr, None), self.plane.ctx)
         return out
 
 
 def rmsnorm(plane, x, w, eps):
-    import torch
-
     rows, n = x.shape
-    out = torch.empty_like(x)
-    check(lib.bh_rmsnorm(plane.ctx, ptr(x), ptr(w), eps, ptr(out), rows, n, _stream()), plane.ctx)
+    out = DeviceArray(plane, x.shape, np.float32)
+    check(lib.bh_rmsnorm(plane.ctx, x.ptr, w.ptr, eps, out.ptr, rows, n, None), plane.ctx)
     return out
 
 
 def rope_(plane, v, pos, n_heads, head_dim, theta, max_pos):
-    rows = pos.numel()
-    check(lib.bh_rope(plane.ctx, ptr(v), ptr(pos), rows, n_heads, head_dim, theta, max_pos, _stream()), plane.ctx)
+    check(lib.bh_rope(plane.ctx, v.ptr, pos.ptr, pos.shape[0], n_heads, head_dim, theta, max_pos, None), plane.ctx)
     return v
 
 
 def silu_mul(plane, g, u):
-    import torch
-
-    out = torch.empty_like(g)
-    check(lib.bh_silu_mul(plane.ctx, ptr(g), ptr(u), ptr(out), g.numel(), _stream()), plane.ctx)
+    out = DeviceArray(plane, g.shape, np.float32)
+    check(lib.bh_silu_mul(plane.ctx, g.ptr, u.ptr, out.ptr, int(np.prod(g.shape)), None), plane.ctx)
     return out
 
 
 def attn_decode(plane, q, k, v, seq_off, seq_len, n_q, n_kv, head_dim, max_len):
     """q: [B, n_q*hd] f32; k, v: [n_kv, rows, hd] (f16 or f32); seq_off int64 [B];
-    seq_len int32 [B]."""
-    import torch
-
-    batch = q.shape[0]
-    out = torch.empty_like(q)
-    kv_f16 = 1 if k.dtype == torch.float16 else 0
-    check(lib.bh_attn_decode(plane.ctx, ptr(q), ptr(k), ptr(v), kv_f16, k.shape[1], ptr(seq_off), ptr(seq_len),
-                             batch, n_q, n_kv, head_dim, max_len, ptr(out), _stream()), plane.ctx)
+    seq_len int32 [B] (all DeviceArrays)."""
+    out = DeviceArray(plane, q.shape, np.float32)
+    kv_f16 = 1 if k.dtype == np.float16 else 0
+    check(lib.bh_attn_decode(plane.ctx, q.ptr, k.ptr, v.ptr, kv_f16, k.shape[1], seq_off.ptr, seq_len.ptr,
+                             q.shape[0], n_q, n_kv, head_dim, max_len, out.ptr, None), plane.ctx)
     return out
+
+
+def synchronize(plane):
+    check(lib.bh_synchronize(plane.ctx), plane.ctx)

@@ -75,6 +75,16 @@ int bh_registry_stats(bh_ctx* ctx, size_t* n_entries, size_t* bytes);
 enum { BH_OP_ANY = 0, BH_OP_MATVEC = 1, BH_OP_UPLOAD = 2, BH_OP_GEMV = 3, BH_OP_DECODE = 4 };
 int bh_debug_inject_fault(bh_ctx* ctx, int op, int status, int count);
 
+/* ------------------------------------------------------- device memory */
+/* Plain device buffers for callers without their own allocator. Copies are blocking
+ * and ordered after all work queued on the context's stream. */
+int bh_dev_alloc(bh_ctx* ctx, size_t bytes, void** out);
+int bh_dev_free(bh_ctx* ctx, void* p);
+int bh_memcpy_h2d(bh_ctx* ctx, void* dst, const void* src, size_t bytes);
+int bh_memcpy_d2h(bh_ctx* ctx, void* dst, const void* src, size_t bytes);
+/* Wait for all work on the device (every stream of this process). */
+int bh_synchronize(bh_ctx* ctx);
+
 /* ------------------------------------------- WgpuComputePlane GEMV mirror */
 /* y = W h for one host vector h [in_features] -> host out [out_features].
  * With model_name and layer_name both non-NULL the weight is uploaded once and kept

@@ -38,14 +38,14 @@ def test_dequant_bit_exact(plane, fmt, n, k):
     w[0] = 0
     q, s, deq = _quant(fmt, w)
     dw = ops.DeviceWeight(plane, fmt, n, k, q, s)
-    got = dw.dequant().cpu().numpy()
+    got = dw.dequant().numpy()
     assert np.array_equal(got.view(np.uint32), deq.view(np.uint32))
 
 
 def test_dequant_bit_exact_lm_head(plane):
     w = _w(9, 151936, 896)
     q, s, deq = _quant(BH_Q4_G32, w)
-    got = ops.DeviceWeight(plane, BH_Q4_G32, 151936, 896, q, s).dequant().cpu().numpy()
+    got = ops.DeviceWeight(plane, BH_Q4_G32, 151936, 896, q, s).dequant().numpy()
     assert np.array_equal(got.view(np.uint32), deq.view(np.uint32))
 
 
@@ -70,12 +70,10 @@ def _q4_cached(n, k):
 @pytest.mark.parametrize("n,k", QWEN_SHAPES)
 @pytest.mark.parametrize("batch", [1, 4, 16, 32])
 def test_gemv_q4g32_qwen_shapes(plane, n, k, batch):
-    import torch
-
     q, s, deq = _q4_cached(n, k)
     x = np.random.default_rng(batch).standard_normal((batch, k)).astype(np.float32)
     dw = ops.DeviceWeight(plane, BH_Q4_G32, n, k, q, s)
-    y = dw.gemv(torch.from_numpy(x).cuda()).cpu().numpy()
+    y = dw.gemv(ops.DeviceArray.from_numpy(plane, x)).numpy()
     _check_gemv(y, deq, x)
     if batch == 1:  # the reference GEMV over the dequantized weights
         yo = oracle.matvec_mul_into(oracle.F32, x[0], deq, None, n)
@@ -85,12 +83,10 @@ def test_gemv_q4g32_qwen_shapes(plane, n, k, batch):
 @pytest.mark.parametrize("fmt", [BH_F32, BH_Q8_ROW, BH_Q4_ROW])
 @pytest.mark.parametrize("n,k,batch", [(896, 896, 1), (4864, 896, 3), (896, 4864, 8), (300, 96, 5)])
 def test_gemv_row_formats(plane, fmt, n, k, batch):
-    import torch
-
     w = _w(fmt * 31 + n, n, k)
     q, s, deq = _quant(fmt, w)
     x = np.random.default_rng(n).standard_normal((batch, k)).astype(np.float32)
-    y = ops.DeviceWeight(plane, fmt, n, k, q, s).gemv(torch.from_numpy(x).cuda()).cpu().numpy()
+    y = ops.DeviceWeight(plane, fmt, n, k, q, s).gemv(ops.DeviceArray.from_numpy(plane, x)).numpy()
     _check_gemv(y, deq, x)
     yo = oracle.matvec_mul_into(fmt, x[0], q, s, n)
     assert np.max(np.abs(y[0] - yo)) <= 1e-5 * max(1.0, np.abs(yo).max())
@@ -155,32 +151,30 @@ def test_registry_errors_and_faults(plane):
 
 
 def test_rmsnorm_rope_silu(plane):
-    import torch
-
+    D = lambda a: ops.DeviceArray.from_numpy(plane, a)  # noqa: E731
     rng = np.random.default_rng(3)
     x = (rng.standard_normal((5, 896)) * 3).astype(np.float32)
     w = (1 + 0.1 * rng.standard_normal(896)).astype(np.float32)
-    got = ops.rmsnorm(plane, torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda(), 1e-6).cpu().numpy()
+    got = ops.rmsnorm(plane, D(x), D(w), 1e-6).numpy()
     want = np.stack([oracle.rms_norm(r, w, 1e-6) for r in x])
     assert np.max(np.abs(got - want)) < 1e-5 * np.abs(want).max()
     pos = np.array([0, 1, 31, 4095, 32767], np.int32)
     v = rng.standard_normal((5, 14 * 64)).astype(np.float32)
-    vt = torch.from_numpy(v).cuda()
-    ops.rope_(plane, vt, torch.from_numpy(pos).cuda(), 14, 64, 1e6, 40960)
-    got = vt.cpu().numpy()
+    vt = D(v)
+    ops.rope_(plane, vt, D(pos), 14, 64, 1e6, 40960)
+    got = vt.numpy()
     for i, p in enumerate(pos):
         want = oracle.apply_rope(v[i], int(p), 14, 64, 1e6)
         assert np.max(np.abs(got[i] - want)) < 2e-6 * max(1.0, np.abs(want).max()), p
     g = (rng.standard_normal(4864) * 3).astype(np.float32)
     u = rng.standard_normal(4864).astype(np.float32)
-    got = ops.silu_mul(plane, torch.from_numpy(g).cuda(), torch.from_numpy(u).cuda()).cpu().numpy()
+    got = ops.silu_mul(plane, D(g), D(u)).numpy()
     want = oracle.silu_mul(g, u)
     assert np.max(np.abs(got - want)) < 2e-6 * np.abs(want).max()
 
 
 def _attn_case(plane, lens, nq=14, nkv=2, hd=64, kv_f16=True, seed=0, check_rows=None):
-    import torch
-
+    D = lambda a: ops.DeviceArray.from_numpy(plane, a)  # noqa: E731
     rng = np.random.default_rng(seed)
     B = len(lens)
     offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)  # prefix sums
@@ -189,9 +183,8 @@ def _attn_case(plane, lens, nq=14, nkv=2, hd=64, kv_f16=True, seed=0, check_rows
     k = rng.standard_normal((nkv, rows, hd)).astype(kdt)
     v = rng.standard_normal((nkv, rows, hd)).astype(kdt)
     q = rng.standard_normal((B, nq * hd)).astype(np.float32)
-    out = ops.attn_decode(plane, torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
-                          torch.from_numpy(offs).cuda(), torch.from_numpy(np.array(lens, np.int32)).cuda(), nq, nkv,
-                          hd, int(max(lens))).cpu().numpy()
+    out = ops.attn_decode(plane, D(q), D(k), D(v), D(offs), D(np.array(lens, np.int32)), nq, nkv, hd,
+                          int(max(lens))).numpy()
     for b in (check_rows if check_rows is not None else range(B)):
         kc = k[:, offs[b]:offs[b] + lens[b]].astype(np.float32).transpose(1, 0, 2)  # -> [T][nkv][hd]
         vc = v[:, offs[b]:offs[b] + lens[b]].astype(np.float32).transpose(1, 0, 2)
