@@ -1,0 +1,138 @@
+// k_epilogue.h — epilogues shared by the GEMV and MFMA GEMM kernels.
+//
+// Input: fin[(j * B + b) * ROWS + r] holds the finished sums (unscaled for the row formats)
+// of weight j (gate/up pair: j = 0, 1), batch row b, weight row row0 + r; kws is the
+// workgroup's K split (EPI_PART). `scratch` has room for B * ROWS floats. All threads
+// of the workgroup call it.
+#pragma once
+
+#include <hip/hip_fp16.h>
+
+#include "bh_internal.h"
+
+namespace bh {
+
+// Per-row factor applied after the sum (row formats); 1 for F32 and Q4_G32.
+template <int FMT>
+__device__ __forceinline__ float row_scale(const void* S, int64_t n) {
+    if constexpr (FMT == BH_Q4_ROW) return ((const float*)S)[n] * 0.0625f;
+    else if constexpr (FMT == BH_Q8_ROW) return ((const float*)S)[n];
+    else return 1.0f;
+}
+
+__device__ __forceinline__ int64_t kv_phys_row(const KvView& kv, int p) {
+    if (kv.max_context > 0 && p >= kv.sink) return kv.sink + (p - kv.sink) % (kv.max_context - kv.sink);
+    return p;
+}
+
+__device__ __forceinline__ void argmax_combine(float& v, int& i, float ov, int oi) {
+    if (ov > v || (ov == v && oi < i)) {
+        v = ov;
+        i = oi;
+    }
+}
+
+
+template <int FMT, int B, int EPI, int ROWS>
+__device__ __forceinline__ void run_epilogue(const GemvArgs& a, const float* fin, float* scratch, int64_t row0,
+                                             int kws) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int nwaves = blockDim.x >> 6;
+    if constexpr (EPI == EPI_PART) {
+        float* part = a.part + (int64_t)kws * a.part_ld;
+        for (int i = threadIdx.x; i < B * ROWS; i += blockDim.x) {
+            const int b = i / ROWS, rr = i % ROWS;
+            const int64_t nn = row0 + rr;
+            if (nn >= a.N || b >= a.batch) continue;
+            part[(int64_t)b * a.N + nn] = fin[i] * row_scale<FMT>(a.S, nn);
+        }
+    } else if constexpr (EPI == EPI_STORE || EPI == EPI_RESID) {
+        for (int i = threadIdx.x; i < B * ROWS; i += blockDim.x) {
+            const int b = i / ROWS, rr = i % ROWS;
+            const int64_t nn = row0 + rr;
+            if (nn >= a.N || b >= a.batch) continue;
+            float v = fin[i] * row_scale<FMT>(a.S, nn);
+            if (a.bias) v += a.bias[nn];
+            float* yp = a.y + (int64_t)b * a.ldy + nn;
+            if constexpr (EPI == EPI_RESID) *yp = *yp + v;
+            else *yp = v;
+        }
+    } else if constexpr (EPI == EPI_SILU) {
+        for (int i = threadIdx.x; i < B * ROWS; i += blockDim.x) {
+            const int b = i / ROWS, rr = i % ROWS;
+            const int64_t nn = row0 + rr;
+            if (nn >= a.N || b >= a.batch) continue;
+            const float g = fin[i] * row_scale<FMT>(a.S, nn);
+            const float u = fin[B * ROWS + i] * row_scale<FMT>(a.S2, nn);
+            a.y[(int64_t)b * a.ldy + nn] = g * (1.0f / (1.0f + expf(-g))) * u;
+        }
+    } else if constexpr (EPI == EPI_QKV) {
+        const int half = a.hd >> 1;
+        for (int i = threadIdx.x; i < B * ROWS; i += blockDim.x) {
+            const int b = i / ROWS, rr = i % ROWS;
+            const int64_t nn = row0 + rr;
+            if (nn >= a.N || b >= a.batch) continue;
+            float val = fin[i] * row_scale<FMT>(a.S, nn);
+            if (a.bias) val += a.bias[nn];
+            const int sec = nn < a.qd ? 0 : (nn < a.qd + a.kd ? 1 : 2);
+            const int loc = (int)nn - (sec == 0 ? 0 : (sec == 1 ? a.qd : a.qd + a.kd));
+            const int hh = loc / a.hd, d = loc % a.hd;
+            const int p = a.pos[b];
+            if (sec < 2) {  // rotate-half RoPE (apply_rope_cpu, cpu_engine.rs:1682-1699)
+                const int dp = d < half ? half : -half;
+                float pv = fin[i + dp] * row_scale<FMT>(a.S, nn + dp);
+                if (a.bias) pv += a.bias[nn + dp];
+                const float2 cs = a.rope[(int64_t)p * half + (d < half ? d : d - half)];
+                val = d < half ? (val * cs.x - pv * cs.y) : (val * cs.x + pv * cs.y);
+            }
+            if (sec == 0) {
+                a.y[(int64_t)b * a.ldy + nn] = val;
+            } else {
+                const int64_t row = a.seq_off[a.slot[b]] + kv_phys_row(a.kv, p);
+                const int64_t off = ((int64_t)hh * a.kv.kv_rows + row) * a.hd + d;
+                void* base = sec == 1 ? a.kv.k : a.kv.v;
+                if (a.kv.kv_f16) ((__half*)base)[off] = __float2half(val);
+                else ((float*)base)[off] = val;
+            }
+        }
+    } else if constexpr (EPI == EPI_LMHEAD) {
+        // raw logits out, then repetition penalty (cpu_engine.rs:2984-2992) in LDS
+        for (int i = threadIdx.x; i < B * ROWS; i += blockDim.x) {
+            const int b = i / ROWS, rr = i % ROWS;
+            const int64_t nn = row0 + rr;
+            float pv = -INFINITY;
+            if (nn < a.N && b < a.batch) {
+                float v = fin[i] * row_scale<FMT>(a.S, nn);
+                a.y[(int64_t)b * a.ldy + nn] = v;
+                const int cnt = a.pen[(int64_t)a.slot[b] * a.vocab + nn];
+                for (int t = 0; t < cnt; ++t) v = v > 0.f ? v / 1.15f : v * 1.15f;
+                pv = v > -INFINITY ? v : -INFINITY;  // NaN never wins (first-max scan uses `>`)
+            }
+            scratch[i] = pv;
+        }
+        __syncthreads();
+        // one argmax per 64-row sub-tile: partials stay indexed by 64-row tiles
+        constexpr int SUB = ROWS / 64;
+        const int tiles64 = (int)((a.n_pad + 63) / 64);
+        for (int q = wave; q < B * SUB; q += nwaves) {
+            const int b = q / SUB, sub = q % SUB;
+            if (b >= a.batch) continue;
+            float v = scratch[b * ROWS + sub * 64 + lane];
+            int idx = v > -INFINITY ? (int)(row0 + sub * 64 + lane) : 0x7fffffff;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                const float ov = __shfl_xor(v, off);
+                const int oi = __shfl_xor(idx, off);
+                argmax_combine(v, idx, ov, oi);
+            }
+            const int64_t t64 = row0 / 64 + sub;
+            if (lane == 0 && t64 < tiles64) {
+                a.part_val[(int64_t)b * tiles64 + t64] = v;
+                a.part_idx[(int64_t)b * tiles64 + t64] = idx;
+            }
+        }
+    }
+}
+
+}  // namespace bh

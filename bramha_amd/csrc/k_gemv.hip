@@ -24,6 +24,8 @@
 
 #include <hip/hip_fp16.h>
 
+#include "k_epilogue.h"
+
 namespace bh {
 namespace {
 
@@ -80,28 +82,114 @@ __device__ __forceinline__ void decode(const uint4 q, float* v) {
     }
 }
 
-// Per-row factor applied after the sum (row formats); 1 for F32 and Q4_G32.
-template <int FMT>
-__device__ __forceinline__ float row_scale(const void* S, int64_t n) {
-    if constexpr (FMT == BH_Q4_ROW) return ((const float*)S)[n] * 0.0625f;
-    else if constexpr (FMT == BH_Q8_ROW) return ((const float*)S)[n];
-    else return 1.0f;
+// ---- MFMA path (16 or 32 tokens per pass, 4-bit weights) ----
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// One dword of a Q4 chunk (8 weights) -> 8 exact fp16 values q - 8 for the A operand of
+// v_mfma_f32_16x16x32_f16. Register pair j holds (nibble j, nibble j + 4): 1024 + q is
+// formed in the fp16 mantissa and 1032 subtracted. Nibble t is element t ^ 1 of the 8
+// (the high nibble of a byte is the even element), so K slot s of the lane holds element
+// kperm(s) = {1, 5, 0, 4, 3, 7, 2, 6}[s]; the activations use the same permutation (the MFMA
+// sum over K is order-free). A function, not a table, so that every index folds at compile time.
+__host__ __device__ constexpr int kperm(int s) { return ((s >> 1) ^ 1) + 4 * (s & 1); }
+
+__device__ __forceinline__ half8 dec8(uint32_t w) {
+    const half2v off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+    half8 r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t p = ((w >> (4 * j)) & 0x000F000Fu) | 0x64006400u;
+        const half2v h = __builtin_bit_cast(half2v, p) + off;
+        r[2 * j] = h.x;
+        r[2 * j + 1] = h.y;
+    }
+    return r;
 }
 
-__device__ __forceinline__ int64_t kv_phys_row(const KvView& kv, int p) {
-    if (kv.max_context > 0 && p >= kv.sink) return kv.sink + (p - kv.sink) % (kv.max_context - kv.sink);
-    return p;
+// f32 activations -> fp16 hi + lo (hi + lo carries ~22 bits of the f32 mantissa).
+__device__ __forceinline__ void split8(const float4& x0, const float4& x1, half8& hi, half8& lo) {
+    const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        const float f = xv[kperm(s)];
+        const _Float16 h = (_Float16)f;
+        hi[s] = h;
+        lo[s] = (_Float16)(f - (float)h);
+    }
 }
 
-__device__ __forceinline__ void argmax_combine(float& v, int& i, float ov, int oi) {
-    if (ov > v || (ov == v && oi < i)) {
-        v = ov;
-        i = oi;
+// One pipeline stage of the MFMA loop: a chunk's weight dwords, group scales and activations.
+template <int NACC, int TB>
+struct MfStage {
+    uint32_t aw[NACC][4];
+    uint2 sw[NACC][4];
+    float4 xv[TB][2];
+};
+
+template <int FMT, int NACC, int TB>
+__device__ __forceinline__ void mf_fetch(const GemvArgs& a, const uint32_t* const (&Wd)[NACC],
+                                         const __half* const (&Sh)[NACC], int c, int64_t n0, int lr, int lg,
+                                         MfStage<NACC, TB>& st) {
+#pragma unroll
+    for (int j = 0; j < NACC; ++j)
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            st.aw[j][rb] = Wd[j][((int64_t)c * a.n_pad + n0 + rb * 16 + lr) * 4 + lg];
+            if constexpr (FMT == BH_Q4_G32)
+                st.sw[j][rb] = *(const uint2*)(Sh[j] + (int64_t)c * a.n_pad + n0 + rb * 16 + 4 * lg);
+        }
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+        // rows past the batch read the last row (in bounds) and are zeroed by value selects,
+        // which keeps the stage in registers (a pointer select would move it to scratch)
+        const int m = tb * 16 + lr;
+        const bool ok = m < a.batch;
+        const float4* xp = (const float4*)(a.x + (int64_t)(ok ? m : a.batch - 1) * a.ldx + c * 32 + 8 * lg);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float4 v = xp[h];
+            st.xv[tb][h] = make_float4(ok ? v.x : 0.f, ok ? v.y : 0.f, ok ? v.z : 0.f, ok ? v.w : 0.f);
+        }
+    }
+}
+
+template <int FMT, int NACC, int TB>
+__device__ __forceinline__ void mf_consume(const MfStage<NACC, TB>& st, f32x4 (&acc)[NACC][4][TB]) {
+    half8 bh[TB], bl[TB];
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) split8(st.xv[tb][0], st.xv[tb][1], bh[tb], bl[tb]);
+#pragma unroll
+    for (int j = 0; j < NACC; ++j) {
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            const half8 av = dec8(st.aw[j][rb]);
+            if constexpr (FMT == BH_Q4_G32) {
+                const __half2* s2 = (const __half2*)&st.sw[j][rb];
+                const float2 sa = __half22float2(s2[0]), sb = __half22float2(s2[1]);
+#pragma unroll
+                for (int tb = 0; tb < TB; ++tb) {
+                    f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bh[tb], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bl[tb], t, 0, 0, 0);
+                    acc[j][rb][tb][0] = fmaf(sa.x, t[0], acc[j][rb][tb][0]);
+                    acc[j][rb][tb][1] = fmaf(sa.y, t[1], acc[j][rb][tb][1]);
+                    acc[j][rb][tb][2] = fmaf(sb.x, t[2], acc[j][rb][tb][2]);
+                    acc[j][rb][tb][3] = fmaf(sb.y, t[3], acc[j][rb][tb][3]);
+                }
+            } else {
+#pragma unroll
+                for (int tb = 0; tb < TB; ++tb) {
+                    acc[j][rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bh[tb], acc[j][rb][tb], 0, 0, 0);
+                    acc[j][rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bl[tb], acc[j][rb][tb], 0, 0, 0);
+                }
+            }
+        }
     }
 }
 
 template <int FMT, int B, int EPI, int RW>
-__global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
+__global__ void __launch_bounds__(B >= 16 ? 256 : 1024) k_gemv(const GemvArgs a) {
     extern __shared__ float smem[];
     constexpr int E = Fmt<FMT>::E;
     constexpr int NACC = EPI == EPI_SILU ? 2 : 1;
@@ -136,6 +224,59 @@ __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
         Sp[1] = (const __half*)a.S2 + n;
     }
 
+    if constexpr (B >= 16) {
+        static_assert(FMT == BH_Q4_G32 || FMT == BH_Q4_ROW, "MFMA path is for 4-bit weights");
+        constexpr int TB = B / 16;
+        const int lr = lane & 15, lg = lane >> 4;
+        const int64_t n0 = (int64_t)tile * ROWS + rw * 64;
+        f32x4 acc[NACC][4][TB];
+#pragma unroll
+        for (int j = 0; j < NACC; ++j)
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                for (int tb = 0; tb < TB; ++tb) acc[j][rb][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const uint32_t* Wd[NACC];
+        Wd[0] = (const uint32_t*)a.W;
+        if constexpr (NACC == 2) Wd[1] = (const uint32_t*)a.W2;
+        const __half* Sh[NACC];
+        Sh[0] = (const __half*)a.S;
+        if constexpr (NACC == 2) Sh[1] = (const __half*)a.S2;
+        if (n0 < a.n_pad && c0 < c1) {
+            // two stages in flight; the refetch past the end re-reads the last chunk (in bounds, unused)
+            MfStage<NACC, TB> s0, s1;
+            mf_fetch<FMT>(a, Wd, Sh, c0, n0, lr, lg, s0);
+            int c = c0;
+            for (; c + 1 < c1; c += 2) {
+                mf_fetch<FMT>(a, Wd, Sh, c + 1, n0, lr, lg, s1);
+                mf_consume<FMT>(s0, acc);
+                mf_fetch<FMT>(a, Wd, Sh, min(c + 2, c1 - 1), n0, lr, lg, s0);
+                mf_consume<FMT>(s1, acc);
+            }
+            if (c < c1) mf_consume<FMT>(s0, acc);
+        }
+        // D layout of 16x16 MFMA: lane holds column lr (token), rows 4*lg + v
+        constexpr float FIN = FMT == BH_Q4_ROW ? 16.0f : 1.0f;  // row formats: the epilogue scales by s/16
+#pragma unroll
+        for (int j = 0; j < NACC; ++j)
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        smem[kw * TOT + (j * B + tb * 16 + lr) * ROWS + rw * 64 + rb * 16 + 4 * lg + v] =
+                            acc[j][rb][tb][v] * FIN;
+        __syncthreads();
+        for (int i = threadIdx.x; i < TOT; i += blockDim.x) {
+            float sum = smem[i];
+            for (int w = 1; w < ksplit; ++w) sum += smem[w * TOT + i];
+            smem[i] = sum;
+        }
+        __syncthreads();
+        run_epilogue<FMT, B, EPI, ROWS>(a, smem, smem + TOT, (int64_t)tile * ROWS, kws);
+        return;
+    } else {
     uint4 q0[NACC][U], q1[NACC][U];
     float s0[NACC][U], s1[NACC][U];
     auto fetch = [&](int c, uint4 (&q)[NACC][U], float (&s)[NACC][U]) {
@@ -202,96 +343,7 @@ __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
     __syncthreads();
     const int64_t row0 = (int64_t)tile * ROWS;
 
-    const float* fin = smem;
-
-    if constexpr (EPI == EPI_PART) {
-        float* part = a.part + (int64_t)kws * a.part_ld;
-        for (int i = threadIdx.x; i < B * ROWS; i += blockDim.x) {
-            const int b = i / ROWS, rr = i % ROWS;
-            const int64_t nn = row0 + rr;
-            if (nn >= a.N || b >= a.batch) continue;
-            part[(int64_t)b * a.N + nn] = fin[i] * row_scale<FMT>(a.S, nn);
-        }
-    } else if constexpr (EPI == EPI_STORE || EPI == EPI_RESID) {
-        for (int i = threadIdx.x; i < B * ROWS; i += blockDim.x) {
-            const int b = i / ROWS, rr = i % ROWS;
-            const int64_t nn = row0 + rr;
-            if (nn >= a.N || b >= a.batch) continue;
-            float v = fin[i] * row_scale<FMT>(a.S, nn);
-            if (a.bias) v += a.bias[nn];
-            float* yp = a.y + (int64_t)b * a.ldy + nn;
-            if constexpr (EPI == EPI_RESID) *yp = *yp + v;
-            else *yp = v;
-        }
-    } else if constexpr (EPI == EPI_SILU) {
-        for (int i = threadIdx.x; i < B * ROWS; i += blockDim.x) {
-            const int b = i / ROWS, rr = i % ROWS;
-            const int64_t nn = row0 + rr;
-            if (nn >= a.N || b >= a.batch) continue;
-            const float g = fin[i] * row_scale<FMT>(a.S, nn);
-            const float u = fin[B * ROWS + i] * row_scale<FMT>(a.S2, nn);
-            a.y[(int64_t)b * a.ldy + nn] = g * (1.0f / (1.0f + expf(-g))) * u;
-        }
-    } else if constexpr (EPI == EPI_QKV) {
-        const int half = a.hd >> 1;
-        for (int i = threadIdx.x; i < B * ROWS; i += blockDim.x) {
-            const int b = i / ROWS, rr = i % ROWS;
-            const int64_t nn = row0 + rr;
-            if (nn >= a.N || b >= a.batch) continue;
-            float val = fin[i] * row_scale<FMT>(a.S, nn);
-            if (a.bias) val += a.bias[nn];
-            const int sec = nn < a.qd ? 0 : (nn < a.qd + a.kd ? 1 : 2);
-            const int loc = (int)nn - (sec == 0 ? 0 : (sec == 1 ? a.qd : a.qd + a.kd));
-            const int hh = loc / a.hd, d = loc % a.hd;
-            const int p = a.pos[b];
-            if (sec < 2) {  // rotate-half RoPE (apply_rope_cpu, cpu_engine.rs:1682-1699)
-                const int dp = d < half ? half : -half;
-                float pv = fin[i + dp] * row_scale<FMT>(a.S, nn + dp);
-                if (a.bias) pv += a.bias[nn + dp];
-                const float2 cs = a.rope[(int64_t)p * half + (d < half ? d : d - half)];
-                val = d < half ? (val * cs.x - pv * cs.y) : (val * cs.x + pv * cs.y);
-            }
-            if (sec == 0) {
-                a.y[(int64_t)b * a.ldy + nn] = val;
-            } else {
-                const int64_t row = a.seq_off[a.slot[b]] + kv_phys_row(a.kv, p);
-                const int64_t off = ((int64_t)hh * a.kv.kv_rows + row) * a.hd + d;
-                void* base = sec == 1 ? a.kv.k : a.kv.v;
-                if (a.kv.kv_f16) ((__half*)base)[off] = __float2half(val);
-                else ((float*)base)[off] = val;
-            }
-        }
-    } else if constexpr (EPI == EPI_LMHEAD) {
-        // raw logits out, then repetition penalty (cpu_engine.rs:2984-2992) in LDS
-        for (int i = threadIdx.x; i < B * ROWS; i += blockDim.x) {
-            const int b = i / ROWS, rr = i % ROWS;
-            const int64_t nn = row0 + rr;
-            float pv = -INFINITY;
-            if (nn < a.N && b < a.batch) {
-                float v = fin[i] * row_scale<FMT>(a.S, nn);
-                a.y[(int64_t)b * a.ldy + nn] = v;
-                const int cnt = a.pen[(int64_t)a.slot[b] * a.vocab + nn];
-                for (int t = 0; t < cnt; ++t) v = v > 0.f ? v / 1.15f : v * 1.15f;
-                pv = v > -INFINITY ? v : -INFINITY;  // NaN never wins (first-max scan uses `>`)
-            }
-            smem[TOT + i] = pv;
-        }
-        __syncthreads();
-        for (int b = wave; b < B; b += nwaves) {
-            if (b >= a.batch) continue;
-            float v = smem[TOT + b * ROWS + lane];
-            int idx = v > -INFINITY ? (int)(row0 + lane) : 0x7fffffff;
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) {
-                const float ov = __shfl_xor(v, off);
-                const int oi = __shfl_xor(idx, off);
-                argmax_combine(v, idx, ov, oi);
-            }
-            if (lane == 0) {
-                a.part_val[(int64_t)b * tiles + tile] = v;
-                a.part_idx[(int64_t)b * tiles + tile] = idx;
-            }
-        }
+    run_epilogue<FMT, B, EPI, ROWS>(a, smem, smem + TOT, (int64_t)tile * ROWS, kws);
     }
 }
 
@@ -308,6 +360,10 @@ hipError_t launch_one(const GemvArgs& a, int ksplit, int ksw, hipStream_t st) {
 
 template <int FMT, int EPI, int RW>
 hipError_t launch_b(const GemvArgs& a, int B, int ksplit, int ksw, hipStream_t st) {
+    if constexpr (FMT == BH_Q4_G32 || FMT == BH_Q4_ROW) {
+        if (B == 32) return launch_one<FMT, 32, EPI, RW>(a, ksplit, ksw, st);
+        if (B == 16) return launch_one<FMT, 16, EPI, RW>(a, ksplit, ksw, st);
+    }
     switch (B) {
         case 1: return launch_one<FMT, 1, EPI, RW>(a, ksplit, ksw, st);
         case 2: return launch_one<FMT, 2, EPI, RW>(a, ksplit, ksw, st);
@@ -334,10 +390,11 @@ hipError_t launch_fmt(int epi, const GemvArgs& a, int B, int rw, int ksplit, int
 
 }  // namespace
 
-// Waves per workgroup along K: aim for ~8 waves per CU and >= 2 chunks per wave.
+// Waves per workgroup along K: aim for ~8 waves per CU and >= 2 chunks per wave
+// (MFMA passes: at most 256 threads per workgroup).
 static int waves_per_tile(int tiles, int rw, int C, int nacc, int B) {
-    int ks = (2048 + tiles * rw - 1) / (tiles * rw);
-    ks = std::max(1, std::min({ks, 16 / rw, std::max(1, C / 2)}));
+    int ks = ((B >= 16 ? 4096 : 2048) + tiles * rw - 1) / (tiles * rw);
+    ks = std::max(1, std::min({ks, (B >= 16 ? 4 : 16) / rw, std::max(1, C / 2)}));
     while (ks > 1 && (size_t)ks * nacc * B * 64 * rw * 4 > 60 * 1024) --ks;
     return ks;
 }
@@ -360,7 +417,9 @@ hipError_t launch_gemv(int fmt, int epi, const GemvArgs& a0, hipStream_t st) {
     int b0 = 0;
     while (b0 < a0.batch) {
         const int rem = a0.batch - b0;
-        const int B = rem >= 8 ? 8 : (rem >= 4 ? 4 : (rem >= 2 ? 2 : 1));
+        // 4-bit weights with >= 16 rows left: MFMA passes of 32 or 16; else VALU passes <= 8
+        const bool mf = (fmt == BH_Q4_G32 || fmt == BH_Q4_ROW) && rem >= 16;
+        const int B = mf ? (rem >= 32 ? 32 : 16) : (rem >= 8 ? 8 : (rem >= 4 ? 4 : (rem >= 2 ? 2 : 1)));
         int ks = waves_per_tile(tiles * ksw, rw, (a0.C + ksw - 1) / ksw, nacc, B);
         GemvArgs a = a0;
         a.batch = B;

@@ -60,6 +60,35 @@ def test_tiny_long_prompt_crosses_prefill_chunks(plane):
     assert np.max(np.abs(olg - glg)) <= 1e-4 * max(1.0, np.abs(olg).max())
 
 
+@pytest.mark.parametrize("wfmt", [Q4_G32, Q4_ROW])
+def test_tiny_4bit_prefill_mfma(plane, wfmt):
+    # 69 prefill tokens: MFMA passes of 32 + 32, then a 5-token VALU pass
+    cfg = tiny_cfg(wfmt, Q4_G32 if wfmt == Q4_G32 else F32, gqa7=True)
+    om, gm = _pair(plane, cfg, seed=21)
+    p = prompt(70, cfg.vocab, seed=22)
+    oids, olg = om.generate(p, 8, want_logits=True)
+    gids, glg = gm.generate(p, 8, want_logits=True)
+    assert np.array_equal(oids, gids)
+    assert np.max(np.abs(olg - glg)) <= 1e-4 * max(1.0, np.abs(olg).max())
+
+
+def test_batch20_decode_mfma(plane):
+    # 20 sequences decoded together: MFMA pass of 16 + VALU pass of 4 in every projection
+    cfg = tiny_cfg(Q4_G32, Q4_G32, gqa7=True, max_seqs=20, kv_rows=20 * 64)
+    om, gm = _pair(plane, cfg, seed=23)
+    prompts = [prompt(3 + (s * 7) % 30, cfg.vocab, seed=100 + s) for s in range(20)]
+    for s, p in enumerate(prompts):
+        gm.seq_open(s, 64)
+        gm.prefill(s, p[:-1])
+    gm.decode_setup(list(range(20)), [p[-1] for p in prompts])
+    ids, lg = gm.decode(6, want_logits=True)
+    for s, p in enumerate(prompts):
+        want, wl = om.generate(p, 6, want_logits=True)
+        n = len(want)
+        assert np.array_equal(ids[:n, s], want), s
+        assert np.max(np.abs(lg[:n, s] - wl)) <= 1e-4 * max(1.0, np.abs(wl).max()), s
+
+
 def test_tiny_sink_eviction(plane):
     cfg = tiny_cfg(F32, F32, max_context=16, sink_tokens=4)
     om, gm = _pair(plane, cfg, seed=5)

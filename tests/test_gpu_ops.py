@@ -81,7 +81,7 @@ def test_gemv_q4g32_qwen_shapes(plane, n, k, batch):
 
 
 @pytest.mark.parametrize("fmt", [BH_F32, BH_Q8_ROW, BH_Q4_ROW])
-@pytest.mark.parametrize("n,k,batch", [(896, 896, 1), (4864, 896, 3), (896, 4864, 8), (300, 96, 5)])
+@pytest.mark.parametrize("n,k,batch", [(896, 896, 1), (4864, 896, 3), (896, 4864, 8), (300, 96, 5), (896, 4864, 20)])
 def test_gemv_row_formats(plane, fmt, n, k, batch):
     w = _w(fmt * 31 + n, n, k)
     q, s, deq = _quant(fmt, w)
