@@ -136,11 +136,13 @@ def main():
     bs32 = None
     if not args.only_bs1:
         log("building bs32 model")
-        m32, _ = build_model(plane, 32, args.prompt, total)
+        m32, _ = build_model(plane, 32, args.prompt, total + 32)
         dt32 = timed_decode(m32, args.steps, args.warmup)
+        kern32, roof32 = roofline(m32)
         bs32 = {"value": 32 * args.steps / dt32, "unit": "tok/s", "ms_per_step": dt32 * 1e3 / args.steps,
-                "batch": 32}
-        log("bs32: %.1f tok/s (%.3f ms/step)" % (bs32["value"], bs32["ms_per_step"]))
+                "batch": 32, "roofline": roof32}
+        log("bs32: %.1f tok/s (%.3f ms/step); dominant kernel %s: %.1f GB/s" %
+            (bs32["value"], bs32["ms_per_step"], kern32, roof32["achieved"]))
         m32.close()
     cpu = None
     if not args.no_cpu_baseline:

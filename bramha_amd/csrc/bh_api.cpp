@@ -20,6 +20,10 @@
 
 using namespace bh;
 
+namespace bh {
+thread_local LaunchEvents* launch_events = nullptr;
+}
+
 // ------------------------------------------------------------------ helpers
 int bh_ctx::fail(int status, const std::string& msg) {
     err = msg;
@@ -532,7 +536,7 @@ int bh_attn_decode(bh_ctx* ctx, const float* q, const void* k, const void* v, in
     a.kv.v = (void*)v;
     a.kv.kv_rows = kv_rows;
     a.kv.kv_f16 = kv_f16 ? 1 : 0;
-    a.seq_off = seq_off;
+    a.boff = seq_off;
     a.seq_len = seq_len;
     a.batch = batch;
     a.nq = n_q;

@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <cstddef>
 #include <cstdint>
 #include <functional>
@@ -47,16 +48,18 @@ inline double weight_bytes(const DevWeight& w) {
 // Kernel launch parameters
 // ---------------------------------------------------------------------------
 enum Epi : int {
-    EPI_STORE = 0,   // y = acc (+ bias)
-    EPI_RESID = 1,   // y += acc (+ bias)          (O / down projection + residual)
-    EPI_SILU = 2,    // y = silu(acc_gate) * acc_up (gate/up pair)
-    EPI_QKV = 3,     // bias, RoPE, q -> y, k/v -> KV cache
-    EPI_LMHEAD = 4,  // logits -> y, repetition penalty, per-tile argmax -> partial
-    EPI_PART = 5,    // K split over workgroups: scaled partial sums -> part[split][b][n]
+    EPI_STORE = 0,    // y = acc (+ bias)
+    EPI_RESNORM = 1,  // residual producer (O / down): x += acc (+ bias); xw = x * wnext; ssq per 64 rows
+    EPI_SILU = 2,     // y = silu(acc_gate) * acc_up (gate/up pair)
+    EPI_QKV = 3,      // bias, RoPE, q -> y, k/v -> KV cache
+    EPI_LMHEAD = 4,   // logits -> y, repetition penalty, per-64-row argmax -> partial
 };
 
-struct KvView {            // packed KV cache of one layer
-    void* k = nullptr;     // [n_kv][kv_rows][hd]
+// Packed KV cache of one layer. K is [n_kv][kv_rows][hd]. V is [n_kv][kv_rows][hd] in f32 and
+// transposed, [n_kv][hd][kv_rows], in fp16: the fp16 cache is read by the MFMA attention kernel,
+// whose V operand takes 8 consecutive rows of one column per lane.
+struct KvView {
+    void* k = nullptr;
     void* v = nullptr;
     int64_t kv_rows = 0;
     int kv_f16 = 1;
@@ -64,6 +67,11 @@ struct KvView {            // packed KV cache of one layer
     int sink = 0;
 };
 
+// The residual stream between kernels: x [T][H] (f32), xw = x * (the next RMSNorm's weight),
+// and ssq [T][H/64] = sums of x^2 over each 64-element tile. A consumer GEMV reads xw as its
+// activations and scales its sums by rnorm = 1/sqrt(sum(ssq)/H + eps): the RMSNorm of
+// rms_norm_into (cpu_engine.rs:1292-1302) folded into the projection, since
+// sum_k W[n][k] * (x[k] * r * w[k]) = r * sum_k W[n][k] * (x[k] * w[k]).
 struct GemvArgs {
     const void* W = nullptr;
     const void* S = nullptr;
@@ -71,66 +79,104 @@ struct GemvArgs {
     const void* S2 = nullptr;
     const float* x = nullptr;
     int64_t ldx = 0;
-    float* y = nullptr;
+    float* y = nullptr;        // EPI_RESNORM: the residual x, updated in place
     int64_t ldy = 0;
     const float* bias = nullptr;
     int N = 0, n_pad = 0, C = 0;
     int batch = 0;
+    // consumer side of the residual stream: per-token norm factor from ssq (null: none)
+    const float* ssq_in = nullptr;     // [batch][ssq_tiles]
+    int ssq_tiles = 0;
+    float norm_n = 0.f, eps = 0.f;
+    // EPI_RESNORM: xw[b][n] = x[b][n] * wnext[n], ssq_out[b][tile] (stride ssq_tiles)
+    float* xw_out = nullptr;
+    const float* wnext = nullptr;
+    float* ssq_out = nullptr;
+    // K split over workgroups: `ksw` workgroups per row tile each store their sums in
+    // part[tile * ksw + split][NACC][B][ROWS]; the last to arrive (tile_cnt, reset by it) adds them
+    // in split order and runs the epilogue. Needs (tiles * ksw) * NACC * B * ROWS floats of part.
+    int ksw = 1;
+    float* part = nullptr;
+    int32_t* tile_cnt = nullptr;
     // EPI_QKV
     int qd = 0, kd = 0, hd = 0;
-    const int32_t* pos = nullptr;      // [batch]
-    const int32_t* slot = nullptr;     // [batch]
-    const int64_t* seq_off = nullptr;  // [slots]
+    const int32_t* pos = nullptr;      // [batch] absolute positions
+    const int64_t* boff = nullptr;     // [batch] first KV row of each entry's sequence region
     const float2* rope = nullptr;      // [max_pos][hd/2] (cos, sin)
     KvView kv;
     // EPI_LMHEAD
+    const int32_t* slot = nullptr;     // [batch]
     const uint16_t* pen = nullptr;     // [slots][vocab] generated-id counts
     int vocab = 0;
-    float* part_val = nullptr;         // [batch][tiles]
+    float* part_val = nullptr;         // [batch][tiles64]
     int32_t* part_idx = nullptr;
-    // EPI_PART: `ksw` workgroups per row tile each write their scaled partial sums to
-    // part[split][b][n] (stride part_ld per split, N per row); the consumer adds them.
-    float* part = nullptr;
-    int ksw = 1;
-    int64_t part_ld = 0;
 };
+
+// Per-launch timing: while `launch_events` is set (bh_model_time_kernels), every kernel is
+// launched with hipExtLaunchKernelGGL, which records the two events at the kernel's own start
+// and end on its stream (no separate event commands around the launch).
+struct LaunchEvents {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+extern thread_local LaunchEvents* launch_events;
+template <typename K, typename... Args>
+inline void launch_kernel(K kernel, dim3 grid, dim3 block, size_t shm, hipStream_t st, Args... args) {
+    if (launch_events)
+        hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)shm, st, launch_events->start, launch_events->stop, 0u,
+                              args...);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, shm, st, args...);
+}
 
 // Launchers (k_gemv.hip). Return hipSuccess or the launch error.
 hipError_t launch_gemv(int fmt, int epi, const GemvArgs& a, hipStream_t st);
+// Workgroups per row tile for a K-split GEMV over `tiles` row tiles and C chunks.
+int gemv_splits(int tiles, int C, int min_chunks);
+constexpr int MAX_KSW = 16;
+constexpr int SPLIT_WG_MAX = 512;   // tiles * ksw of a split launch
+constexpr int SPLIT_TOT_MAX = 2 * 32 * 128;  // NACC * B * ROWS floats per workgroup
 
 // k_ops.hip
 hipError_t launch_rmsnorm(const float* x, const float* w, float eps, float* out, int rows, int n, hipStream_t st);
-// Residual reduce + RMSNorm per row b: x[b] += sum_{s < splits} part[s][b] (+ bias), in a
-// fixed order, then h[b] = x[b] * (1/sqrt(mean(x[b]^2) + eps)) * w. splits 0: norm only.
-hipError_t launch_resid_norm(float* x, const float* part, int splits, int64_t part_ld, const float* bias,
-                             const float* w, float eps, float* h, int rows, int n, hipStream_t st);
-// Split count for an EPI_PART GEMV over `tiles` row tiles and C chunks.
-int part_splits(int tiles, int C);
 hipError_t launch_rope(float* v, const int32_t* pos, const float2* tab, int rows, int n_heads, int hd, hipStream_t st);
 hipError_t launch_silu_mul(const float* g, const float* u, float* out, int64_t n, hipStream_t st);
 hipError_t launch_dequant(const DevWeight& w, float* out, hipStream_t st);
-// Embedding rows of the tied table (KM16 layout, F32 or Q4_G32) for tokens tok[b] % vocab.
-// decode_prologue != 0: first set tok[b] = next[b], pos[b] = seq_len[slot[b]]++ .
-hipError_t launch_embed(const DevWeight& table, int32_t* tok, int32_t* pos, const int32_t* slot, int32_t* seq_len,
-                        const uint32_t* next, int decode_prologue, float* x, int64_t ldx, int batch, hipStream_t st);
-// Final argmax over the LM head's per-tile partials; writes next ids, bumps penalty counts,
-// appends to the id capture buffer (ids_cap + step * batch) when non-null.
-hipError_t launch_sample_final(const float* part_val, const int32_t* part_idx, int tiles, int batch,
-                               const int32_t* slot, uint16_t* pen, int vocab, uint32_t* next, uint32_t* ids_cap,
-                               const int32_t* step_ctr, hipStream_t st);
-hipError_t launch_step_counter(int32_t* ctr, int reset, hipStream_t st);
+// Start of the residual stream for `batch` tokens tok[b] % vocab: x = embedding row of the tied
+// table (KM16, F32 or Q4_G32), xw = x * w0, ssq per 64 elements. reset_step != null: zero it.
+hipError_t launch_embed(const DevWeight& table, const int32_t* tok, const float* w0, float* x, float* xw, float* ssq,
+                        int ssq_tiles, int32_t* reset_step, int batch, hipStream_t st);
+// End of a decode step, one workgroup per batch entry: first-max argmax over the LM head's
+// per-64-row partials; bumps the penalty count of the chosen id; records it at
+// ids_cap[step[b] * batch + b] (ids_cap may be null) and advances step[b]; sets tok[b] to it and
+// pos[b] += 1; and starts the next step's residual stream from its embedding row (as launch_embed).
+struct SampleArgs {
+    const float* part_val = nullptr;
+    const int32_t* part_idx = nullptr;
+    int tiles = 0, batch = 0, vocab = 0;
+    const int32_t* slot = nullptr;
+    uint16_t* pen = nullptr;
+    uint32_t* ids_cap = nullptr;
+    int32_t* step = nullptr;
+    int32_t* tok = nullptr;
+    int32_t* pos = nullptr;
+    const DevWeight* table = nullptr;
+    const float* w0 = nullptr;
+    float *x = nullptr, *xw = nullptr, *ssq = nullptr;
+    int ssq_tiles = 0;
+};
+hipError_t launch_sample(const SampleArgs& a, hipStream_t st);
 
-// k_attn.hip — attention for `batch` query rows: row b (slot[b], position pos[b]) attends to the
-// rows present for its sequence after its own row was appended.
+// k_attn.hip — attention for `batch` query rows: row b attends to the rows of its sequence
+// region that start at KV row boff[b]: pos[b] + 1 of them (capped at the sink ring's size) after
+// its own row was appended, or seq_len[b] of them in standalone mode.
 struct AttnArgs {
     const float* q = nullptr;  // [batch][nq*hd]
     int32_t* cnt = nullptr;    // [batch][nkv] arrival counters of the split merge (zero when idle)
     float* out = nullptr;      // [batch][nq*hd]
     KvView kv;
     const int32_t* pos = nullptr;
-    const int32_t* slot = nullptr;
-    const int64_t* seq_off = nullptr;
-    const int32_t* seq_len = nullptr;  // standalone mode: explicit lengths [batch] (pos/slot unused)
+    const int64_t* boff = nullptr;     // [batch]
+    const int32_t* seq_len = nullptr;  // standalone mode: explicit lengths [batch] (pos unused)
     int batch = 0, nq = 0, nkv = 0, hd = 0;
     int splits = 1, split_rows = 0;    // context split: rows per split (multiple of 64)
     float* part_o = nullptr;           // [batch][nq][splits][hd]

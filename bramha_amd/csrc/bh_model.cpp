@@ -2,14 +2,17 @@
 // KV cache, prefill, and graph-replayed greedy decode steps.
 //
 // Reference: generate_cpu_inner_logits (src/inference/cpu_engine.rs:2290-3064) with
-// CPU-only mode and temperature 0. One forward pass over M tokens is
-//   embed -> L x [rmsnorm, QKV(+bias, RoPE, KV append), attention, O(+bias)+residual,
-//                 rmsnorm, gate/up + SiLU gate, down + residual]
-//         -> [final rmsnorm, LM head + repetition penalty + argmax]   (decode only)
-// Sequences own consecutive regions of one packed KV buffer per layer (offsets are
-// prefix sums of the regions' capacities); a decode step reads its token from the
-// previous step's argmax and its position from the sequence's row count, both on the
-// device, so the whole step is captured once as a HIP graph and replayed.
+// CPU-only mode and temperature 0. One forward pass over M tokens is 5 kernels per layer:
+//   QKV GEMV (RMSNorm factor, bias, RoPE, KV append) -> attention ->
+//   O GEMV (+bias, residual add, next norm's inputs) -> gate/up GEMV (norm factor, SiLU gate) ->
+//   down GEMV (residual add, next norm's inputs)
+// then, when decoding, the LM head (final norm factor, logits, repetition penalty, per-tile
+// argmax) and the sample kernel (argmax, penalty count, next token and position, and the
+// next step's embedding row). The residual stream between kernels is x, xw = x * (next norm
+// weight) and per-64-element sums of squares, so no kernel runs the RMSNorm on its own.
+// Sequences own consecutive regions of one packed KV buffer per layer (offsets are prefix
+// sums of the regions' capacities); a decode step reads its token and position from the
+// previous step's sample kernel, so the whole step is captured once as a HIP graph and replayed.
 #include <algorithm>
 #include <cstring>
 #include <vector>
@@ -33,7 +36,7 @@ struct LayerW {
 
 struct TimerRec {
     int cls;
-    hipEvent_t a, b;
+    LaunchEvents ev;
 };
 
 }  // namespace
@@ -51,26 +54,29 @@ struct bh_model {
     bool have_norm = false;
 
     std::vector<void*> kc, vc;
-    float *x = nullptr, *h = nullptr, *q = nullptr, *att = nullptr, *mm = nullptr, *logits = nullptr;
+    int ssq_tiles = 0;             // 64-element tiles of the hidden size
+    // residual stream [max_tokens][hidden]: x, xw = x * next norm weight, ssq per tile
+    float *x = nullptr, *xw = nullptr, *ssq = nullptr;
+    float *q = nullptr, *att = nullptr, *mm = nullptr, *logits = nullptr;
     float* part_val = nullptr;
     int32_t* part_idx = nullptr;
     float* attn_part = nullptr;
     int max_splits = 128;
     int32_t* attn_cnt = nullptr;   // [max_tokens][n_kv] split-merge counters
-    float* gemv_part = nullptr;    // split-K partial sums of the O / down projections
-    int64_t part_ld = 0;           // floats per split: max_tokens * hidden
-    // decode batch inputs (read by the captured graph) and prefill inputs, kept apart so a
+    float* split_part = nullptr;   // K-split sums of split projections
+    int32_t* split_cnt = nullptr;  // their per-tile arrival counters (zero when idle)
+    // decode batch state (read by the captured graph) and prefill staging, kept apart so a
     // prefill between decode calls leaves the batch intact
-    int32_t *d_tok = nullptr, *d_pos = nullptr, *d_slot = nullptr;
+    int32_t *d_tok = nullptr, *d_pos = nullptr, *d_slot = nullptr, *d_step = nullptr;
+    int64_t* d_boff = nullptr;
     int32_t *d_ptok = nullptr, *d_ppos = nullptr, *d_pslot = nullptr;
-    int32_t *d_seq_len = nullptr, *d_step = nullptr;
-    int64_t* d_seq_off = nullptr;
-    uint32_t *d_next = nullptr, *d_ids = nullptr;
+    int64_t* d_pboff = nullptr;
+    uint32_t* d_ids = nullptr;
     int64_t ids_steps = 1024;
     uint16_t* d_pen = nullptr;
     const float2* rope = nullptr;
     int max_pos = 0;
-    int32_t* h_stage = nullptr;  // pinned: [3 * max_tokens + 2]
+    void* h_stage = nullptr;  // pinned staging for small host->device copies
 
     std::vector<int64_t> off_h, cap_h;
     std::vector<int32_t> len_h;
@@ -85,7 +91,7 @@ struct bh_model {
 
     bool timing = false;
     std::vector<TimerRec> recs;
-    std::vector<hipEvent_t> ev_pool;
+    std::vector<LaunchEvents> ev_pool;
     size_t ev_used = 0;
 
     std::vector<void*> allocs;  // device buffers owned by the model
@@ -105,23 +111,25 @@ hipError_t dmalloc(bh_model* m, void** p, size_t bytes) {
     return e;
 }
 
-hipEvent_t next_event(bh_model* m) {
+LaunchEvents* next_events(bh_model* m) {
     if (m->ev_used == m->ev_pool.size()) {
-        hipEvent_t e;
-        hipEventCreate(&e);
-        m->ev_pool.push_back(e);
+        LaunchEvents ev;
+        hipEventCreate(&ev.start);
+        hipEventCreate(&ev.stop);
+        m->ev_pool.push_back(ev);
     }
-    return m->ev_pool[m->ev_used++];
+    return &m->ev_pool[m->ev_used++];
 }
 
+// Runs one launcher; in timing mode its kernel records a pair of events at its own start and end.
 template <class F>
 hipError_t timed(bh_model* m, int cls, F&& f) {
     if (!m->timing) return f();
-    hipEvent_t a = next_event(m), b = next_event(m);
-    hipEventRecord(a, m->st);
+    LaunchEvents* ev = next_events(m);
+    launch_events = ev;
     hipError_t e = f();
-    hipEventRecord(b, m->st);
-    m->recs.push_back({cls, a, b});
+    launch_events = nullptr;
+    m->recs.push_back({cls, *ev});
     return e;
 }
 
@@ -136,45 +144,70 @@ KvView kv_view(bh_model* m, int l) {
     return v;
 }
 
-// One forward pass over M tokens: the decode batch (decode = true: tokens from the last
-// argmax, positions from the row counts, logits and sampling) or a staged prefill chunk.
-// Per layer: QKV (+bias, RoPE, KV append) -> attention -> O partial sums -> residual +
-// post-attention norm -> gate/up + SiLU -> down partial sums -> residual + next norm.
+// Consumer side of the residual stream: activations xw, per-token norm factor from ssq.
+void stream_input(bh_model* m, GemvArgs& a) {
+    a.x = m->xw;
+    a.ldx = m->c.hidden;
+    a.ssq_in = m->ssq;
+    a.ssq_tiles = m->ssq_tiles;
+    a.norm_n = (float)m->c.hidden;
+    a.eps = m->c.rms_eps;
+}
+
+// K split over workgroups with the in-kernel ordered reduction, for projections whose few row
+// tiles would leave most CUs idle (each workgroup streams at least min_chunks 16-byte chunks per
+// row; at most max_ksw splits: each split level costs about a microsecond of reduction).
+void split_k(bh_model* m, GemvArgs& a, int min_chunks, int max_ksw) {
+    const int tiles = a.n_pad / 64;
+    a.ksw = std::min(gemv_splits(tiles, a.C, min_chunks), max_ksw);
+    while (a.ksw > 1 && tiles * a.ksw > SPLIT_WG_MAX) --a.ksw;
+    a.part = m->split_part;
+    a.tile_cnt = m->split_cnt;
+}
+
+// Producer side: residual add into x, xw with the next norm's weight, ssq.
+void stream_output(bh_model* m, GemvArgs& a, const float* wnext) {
+    a.y = m->x;
+    a.ldy = m->c.hidden;
+    a.xw_out = m->xw;
+    a.wnext = wnext;
+    a.ssq_out = m->ssq;
+    a.ssq_tiles = m->ssq_tiles;
+}
+
+void weight_args(GemvArgs& a, const DevWeight& w) {
+    a.W = w.q;
+    a.S = w.s;
+    a.N = (int)w.n;
+    a.n_pad = (int)w.n_pad;
+    a.C = (int)w.chunks;
+}
+
+// One forward pass over M tokens whose residual stream (x, xw, ssq) holds their embedding rows:
+// the decode batch (decode = true: logits, penalty, argmax and the next step's stream) or a
+// staged prefill chunk.
 hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) {
     const bh_model_config& c = m->c;
     const int H = c.hidden, I = c.ffn;
     hipStream_t st = m->st;
-    int32_t* tok = decode ? m->d_tok : m->d_ptok;
     int32_t* pos = decode ? m->d_pos : m->d_ppos;
     int32_t* slot = decode ? m->d_slot : m->d_pslot;
-    const bool logits = decode;
-    hipError_t e = timed(m, BH_K_OTHER, [&] {
-        return launch_embed(m->embed, tok, pos, slot, m->d_seq_len, m->d_next, decode ? 1 : 0, m->x, H, M, st);
-    });
-    if (e == hipSuccess)
-        e = timed(m, BH_K_NORM, [&] {
-            return launch_resid_norm(m->x, nullptr, 0, 0, nullptr, m->L[0].ln1, c.rms_eps, m->h, M, H, st);
-        });
+    int64_t* boff = decode ? m->d_boff : m->d_pboff;
+    hipError_t e = hipSuccess;
     for (int l = 0; l < c.n_layers && e == hipSuccess; ++l) {
         LayerW& w = m->L[l];
         GemvArgs a;
-        a.W = w.qkv.q;
-        a.S = w.qkv.s;
-        a.x = m->h;
-        a.ldx = H;
+        weight_args(a, w.qkv);
+        stream_input(m, a);
         a.y = m->q;
         a.ldy = m->QD;
         a.bias = c.attn_bias ? w.bqkv : nullptr;
-        a.N = (int)m->NQKV;
-        a.n_pad = (int)w.qkv.n_pad;
-        a.C = (int)w.qkv.chunks;
         a.batch = M;
         a.qd = (int)m->QD;
         a.kd = (int)m->KD;
         a.hd = c.head_dim;
         a.pos = pos;
-        a.slot = slot;
-        a.seq_off = m->d_seq_off;
+        a.boff = boff;
         a.rope = m->rope;
         a.kv = kv_view(m, l);
         e = timed(m, BH_K_GEMV_QKV, [&] { return launch_gemv(c.wfmt, EPI_QKV, a, st); });
@@ -184,8 +217,7 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
         at.out = m->att;
         at.kv = kv_view(m, l);
         at.pos = pos;
-        at.slot = slot;
-        at.seq_off = m->d_seq_off;
+        at.boff = boff;
         at.batch = M;
         at.nq = c.n_heads;
         at.nkv = c.n_kv_heads;
@@ -198,69 +230,39 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
         e = timed(m, BH_K_ATTN, [&] { return launch_attention(at, st); });
         if (e != hipSuccess) break;
         GemvArgs o;
-        o.W = w.o.q;
-        o.S = w.o.s;
+        weight_args(o, w.o);
         o.x = m->att;
         o.ldx = m->QD;
-        o.N = H;
-        o.n_pad = (int)w.o.n_pad;
-        o.C = (int)w.o.chunks;
+        o.bias = c.o_bias ? w.bo : nullptr;
         o.batch = M;
-        o.part = m->gemv_part;
-        o.part_ld = m->part_ld;
-        o.ksw = part_splits((int)(w.o.n_pad / 64), (int)w.o.chunks);
-        e = timed(m, BH_K_GEMV_O, [&] { return launch_gemv(c.wfmt, EPI_PART, o, st); });
-        if (e != hipSuccess) break;
-        e = timed(m, BH_K_NORM, [&] {
-            return launch_resid_norm(m->x, m->gemv_part, o.ksw, m->part_ld, c.o_bias ? w.bo : nullptr, w.ln2,
-                                     c.rms_eps, m->h, M, H, st);
-        });
+        stream_output(m, o, w.ln2);
+        e = timed(m, BH_K_GEMV_O, [&] { return launch_gemv(c.wfmt, EPI_RESNORM, o, st); });
         if (e != hipSuccess) break;
         GemvArgs gu;
-        gu.W = w.gate.q;
-        gu.S = w.gate.s;
+        weight_args(gu, w.gate);
         gu.W2 = w.up.q;
         gu.S2 = w.up.s;
-        gu.x = m->h;
-        gu.ldx = H;
+        stream_input(m, gu);
         gu.y = m->mm;
         gu.ldy = I;
-        gu.N = I;
-        gu.n_pad = (int)w.gate.n_pad;
-        gu.C = (int)w.gate.chunks;
         gu.batch = M;
         e = timed(m, BH_K_GEMV_GATEUP, [&] { return launch_gemv(c.wfmt, EPI_SILU, gu, st); });
         if (e != hipSuccess) break;
         GemvArgs d;
-        d.W = w.down.q;
-        d.S = w.down.s;
+        weight_args(d, w.down);
         d.x = m->mm;
         d.ldx = I;
-        d.N = H;
-        d.n_pad = (int)w.down.n_pad;
-        d.C = (int)w.down.chunks;
         d.batch = M;
-        d.part = m->gemv_part;
-        d.part_ld = m->part_ld;
-        d.ksw = part_splits((int)(w.down.n_pad / 64), (int)w.down.chunks);
-        e = timed(m, BH_K_GEMV_DOWN, [&] { return launch_gemv(c.wfmt, EPI_PART, d, st); });
-        if (e != hipSuccess) break;
-        const float* next_w = l + 1 < c.n_layers ? m->L[l + 1].ln1 : m->norm;  // final norm after the last layer
-        e = timed(m, BH_K_NORM, [&] {
-            return launch_resid_norm(m->x, m->gemv_part, d.ksw, m->part_ld, nullptr, next_w, c.rms_eps, m->h, M, H, st);
-        });
+        stream_output(m, d, l + 1 < c.n_layers ? m->L[l + 1].ln1 : m->norm);  // final norm after the last layer
+        split_k(m, d, 8, 8);
+        e = timed(m, BH_K_GEMV_DOWN, [&] { return launch_gemv(c.wfmt, EPI_RESNORM, d, st); });
     }
-    if (e != hipSuccess || !logits) return e;
+    if (e != hipSuccess || !decode) return e;
     GemvArgs lm;
-    lm.W = m->embed.q;
-    lm.S = m->embed.s;
-    lm.x = m->h;
-    lm.ldx = H;
+    weight_args(lm, m->embed);
+    stream_input(m, lm);
     lm.y = m->logits;
     lm.ldy = c.vocab;
-    lm.N = c.vocab;
-    lm.n_pad = (int)m->embed.n_pad;
-    lm.C = (int)m->embed.chunks;
     lm.batch = M;
     lm.pen = m->d_pen;
     lm.vocab = c.vocab;
@@ -269,13 +271,33 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
     lm.part_idx = m->part_idx;
     e = timed(m, BH_K_LM_HEAD, [&] { return launch_gemv(c.head_fmt, EPI_LMHEAD, lm, st); });
     if (e != hipSuccess) return e;
-    e = timed(m, BH_K_OTHER, [&] {
-        hipError_t r = launch_sample_final(m->part_val, m->part_idx, m->tiles_lm, M, slot, m->d_pen, c.vocab,
-                                           m->d_next, m->d_ids, m->d_step, st);
-        if (r == hipSuccess) r = launch_step_counter(m->d_step, 0, st);
-        return r;
+    SampleArgs sa;
+    sa.part_val = m->part_val;
+    sa.part_idx = m->part_idx;
+    sa.tiles = m->tiles_lm;
+    sa.batch = M;
+    sa.vocab = c.vocab;
+    sa.slot = slot;
+    sa.pen = m->d_pen;
+    sa.ids_cap = m->d_ids;
+    sa.step = m->d_step;
+    sa.tok = m->d_tok;
+    sa.pos = m->d_pos;
+    sa.table = &m->embed;
+    sa.w0 = m->L[0].ln1;
+    sa.x = m->x;
+    sa.xw = m->xw;
+    sa.ssq = m->ssq;
+    sa.ssq_tiles = m->ssq_tiles;
+    return timed(m, BH_K_OTHER, [&] { return launch_sample(sa, st); });
+}
+
+// Start the decode batch's residual stream from its current tokens and zero the id counters.
+hipError_t decode_start(bh_model* m) {
+    return timed(m, BH_K_OTHER, [&] {
+        return launch_embed(m->embed, m->d_tok, m->L[0].ln1, m->x, m->xw, m->ssq, m->ssq_tiles, m->d_step, m->B,
+                            m->st);
     });
-    return e;
 }
 
 int64_t layer_tensor_count(const bh_model_config& c) { return 9 + (c.attn_bias ? 3 : 0) + (c.o_bias ? 1 : 0); }
@@ -353,6 +375,13 @@ int check_decode_room(bh_model* m, int n_steps) {
     return BH_OK;
 }
 
+// Host -> device copy of a few bytes through the pinned staging buffer, completed before return.
+hipError_t put(bh_model* m, void* dst, const void* src, size_t bytes) {
+    std::memcpy(m->h_stage, src, bytes);
+    hipError_t e = hipMemcpyAsync(dst, m->h_stage, bytes, hipMemcpyHostToDevice, m->st);
+    return e == hipSuccess ? hipStreamSynchronize(m->st) : e;
+}
+
 }  // namespace
 
 extern "C" {
@@ -373,22 +402,24 @@ int bh_model_create(bh_ctx* ctx, const bh_model_config* cfg, bh_model** out) {
     const int64_t QD = (int64_t)c.n_heads * c.head_dim, KD = (int64_t)c.n_kv_heads * c.head_dim;
     if (c.hidden % E || QD % E || c.ffn % E || c.hidden % chunk_elems(c.head_fmt))
         return ctx->fail(BH_ERR_UNSUPPORTED, "hidden, q_dim and ffn must be multiples of the 16-byte chunk");
+    if (c.hidden % 64)
+        return ctx->fail(BH_ERR_UNSUPPORTED, "hidden must be a multiple of 64 (residual-stream tiles)");
     if (c.max_context > 0 && (c.sink_tokens < 0 || c.sink_tokens >= c.max_context))
         return ctx->fail(BH_ERR_INVALID, "sink_tokens must be below max_context");
     if (c.max_tokens > 4096) return ctx->fail(BH_ERR_UNSUPPORTED, "max_tokens above 4096");
-    if (c.hidden > 4096) return ctx->fail(BH_ERR_UNSUPPORTED, "hidden above 4096");
 
     std::lock_guard<std::mutex> g(ctx->mu);
     bh_model* m = new bh_model();
     m->ctx = ctx;
     m->c = c;
+    m->c.kv_rows = (c.kv_rows + 7) / 8 * 8;  // sequence regions start on 8-row boundaries
     m->QD = QD;
     m->KD = KD;
     m->NQKV = QD + 2 * KD;
     m->L.resize(c.n_layers);
     m->max_pos = (int)std::max<int64_t>(65536, c.kv_rows + 1);
     m->tiles_lm = (int)(pad64(c.vocab) / 64);
-    m->part_ld = (int64_t)c.max_tokens * c.hidden;
+    m->ssq_tiles = c.hidden / 64;
     auto bail = [&](hipError_t e, const char* what) {
         int rc = ctx->hip_fail(e, what);
         bh_model_destroy(m);
@@ -396,7 +427,7 @@ int bh_model_create(bh_ctx* ctx, const bh_model_config* cfg, bh_model** out) {
     };
     hipError_t e = hipStreamCreateWithFlags(&m->st, hipStreamNonBlocking);
     if (e != hipSuccess) return bail(e, "hipStreamCreate");
-    const size_t kvb = (size_t)c.kv_rows * KD * (c.kv_f16 ? 2 : 4);
+    const size_t kvb = (size_t)m->c.kv_rows * KD * (c.kv_f16 ? 2 : 4);
     m->kc.assign(c.n_layers, nullptr);
     m->vc.assign(c.n_layers, nullptr);
     for (int l = 0; l < c.n_layers; ++l) {
@@ -409,7 +440,8 @@ int bh_model_create(bh_ctx* ctx, const bh_model_config* cfg, bh_model** out) {
         size_t bytes;
     } bufs[] = {
         {(void**)&m->x, T * c.hidden * 4},
-        {(void**)&m->h, T * c.hidden * 4},
+        {(void**)&m->xw, T * c.hidden * 4},
+        {(void**)&m->ssq, T * m->ssq_tiles * 4},
         {(void**)&m->q, T * QD * 4},
         {(void**)&m->att, T * QD * 4},
         {(void**)&m->mm, T * c.ffn * 4},
@@ -418,23 +450,23 @@ int bh_model_create(bh_ctx* ctx, const bh_model_config* cfg, bh_model** out) {
         {(void**)&m->part_idx, T * m->tiles_lm * 4},
         {(void**)&m->attn_part, T * c.n_heads * m->max_splits * (c.head_dim + 2) * 4},
         {(void**)&m->attn_cnt, T * c.n_kv_heads * 4},
-        {(void**)&m->gemv_part, (size_t)16 * T * c.hidden * 4},
+        {(void**)&m->split_part, (size_t)SPLIT_WG_MAX * SPLIT_TOT_MAX * 4},
+        {(void**)&m->split_cnt, (size_t)4096 * 4},
         {(void**)&m->d_tok, T * 4},
         {(void**)&m->d_pos, T * 4},
         {(void**)&m->d_slot, T * 4},
+        {(void**)&m->d_step, T * 4},
+        {(void**)&m->d_boff, T * 8},
         {(void**)&m->d_ptok, T * 4},
         {(void**)&m->d_ppos, T * 4},
         {(void**)&m->d_pslot, T * 4},
-        {(void**)&m->d_next, T * 4},
+        {(void**)&m->d_pboff, T * 8},
         {(void**)&m->d_ids, (size_t)m->ids_steps * T * 4},
-        {(void**)&m->d_step, 16},
-        {(void**)&m->d_seq_len, (size_t)c.max_seqs * 4},
-        {(void**)&m->d_seq_off, (size_t)c.max_seqs * 8},
         {(void**)&m->d_pen, (size_t)c.max_seqs * c.vocab * 2},
     };
     for (auto& b : bufs)
         if ((e = dmalloc(m, b.p, b.bytes)) != hipSuccess) return bail(e, "hipMalloc(activations)");
-    e = hipHostMalloc((void**)&m->h_stage, (3 * T + 16) * 4, hipHostMallocDefault);
+    e = hipHostMalloc(&m->h_stage, (4 * T + 16) * 8, hipHostMallocDefault);
     if (e != hipSuccess) {
         m->h_stage = nullptr;
         return bail(e, "hipHostMalloc");
@@ -462,7 +494,10 @@ void bh_model_destroy(bh_model* m) {
     }
     free_weight(m->embed);
     for (void* p : m->allocs) hipFree(p);
-    for (auto e : m->ev_pool) hipEventDestroy(e);
+    for (auto& ev : m->ev_pool) {
+        hipEventDestroy(ev.start);
+        hipEventDestroy(ev.stop);
+    }
     if (m->h_stage) hipHostFree(m->h_stage);
     if (m->st) hipStreamDestroy(m->st);
     delete m;
@@ -548,6 +583,9 @@ int bh_model_seq_open(bh_model* m, int slot, int64_t capacity) {
     if (slot < 0 || slot >= m->c.max_seqs) return m->fail(BH_ERR_INVALID, "slot out of range");
     if (m->c.max_context > 0) capacity = m->c.max_context;
     if (capacity <= 0) return m->fail(BH_ERR_INVALID, "capacity must be positive");
+    capacity = (capacity + 7) / 8 * 8;  // keeps every region 8-row aligned (16-byte V^T loads)
+    for (int b = 0; b < m->B; ++b)
+        if (m->bslots[b] == slot) return m->fail(BH_ERR_INVALID, "slot is in the decode batch; replace it first");
     if (m->off_h[slot] < 0 || m->cap_h[slot] < capacity) {
         if (m->next_free + capacity > m->c.kv_rows)
             return m->fail(BH_ERR_CAPACITY, "packed KV buffer full: " + std::to_string(m->next_free) + " + " +
@@ -558,10 +596,8 @@ int bh_model_seq_open(bh_model* m, int slot, int64_t capacity) {
     }
     m->len_h[slot] = 0;
     m->open_h[slot] = 1;
-    hipError_t e = hipMemcpyAsync(m->d_seq_off + slot, &m->off_h[slot], 8, hipMemcpyHostToDevice, m->st);
-    const int32_t zero = 0;
-    if (e == hipSuccess) e = hipMemcpyAsync(m->d_seq_len + slot, &zero, 4, hipMemcpyHostToDevice, m->st);
-    if (e == hipSuccess) e = hipMemsetAsync(m->d_pen + (size_t)slot * m->c.vocab, 0, (size_t)m->c.vocab * 2, m->st);
+    // repetition-penalty counts of the slot start at zero (an eager copy-engine fill, never captured)
+    hipError_t e = hipMemsetAsync(m->d_pen + (size_t)slot * m->c.vocab, 0, (size_t)m->c.vocab * 2, m->st);
     if (e == hipSuccess) e = hipStreamSynchronize(m->st);
     return e == hipSuccess ? BH_OK : m->ctx->hip_fail(e, "seq_open");
 }
@@ -584,29 +620,43 @@ int bh_model_prefill(bh_model* m, int slot, const uint32_t* tokens, int n) {
     int done = 0;
     while (done < n) {
         const int M = std::min(n - done, m->c.max_tokens);
-        int32_t* tok = m->h_stage;
+        int64_t* bo = (int64_t*)m->h_stage;
+        int32_t* tok = (int32_t*)(bo + M);
         int32_t* pos = tok + M;
         int32_t* sl = pos + M;
         for (int i = 0; i < M; ++i) {
+            bo[i] = m->off_h[slot];
             tok[i] = (int32_t)tokens[done + i];
             pos[i] = m->len_h[slot] + done + i;
             sl[i] = slot;
         }
-        hipError_t e = hipMemcpyAsync(m->d_ptok, tok, (size_t)M * 4, hipMemcpyHostToDevice, m->st);
+        hipError_t e = hipMemcpyAsync(m->d_pboff, bo, (size_t)M * 8, hipMemcpyHostToDevice, m->st);
+        if (e == hipSuccess) e = hipMemcpyAsync(m->d_ptok, tok, (size_t)M * 4, hipMemcpyHostToDevice, m->st);
         if (e == hipSuccess) e = hipMemcpyAsync(m->d_ppos, pos, (size_t)M * 4, hipMemcpyHostToDevice, m->st);
         if (e == hipSuccess) e = hipMemcpyAsync(m->d_pslot, sl, (size_t)M * 4, hipMemcpyHostToDevice, m->st);
         int splits, rows;
         attn_plan(pos[M - 1] + 1, M, m->c.n_kv_heads, &splits, &rows);
+        if (e == hipSuccess)
+            e = launch_embed(m->embed, m->d_ptok, m->L[0].ln1, m->x, m->xw, m->ssq, m->ssq_tiles, nullptr, M, m->st);
         if (e == hipSuccess) e = forward(m, M, false, splits, rows);
-        if (e == hipSuccess) e = hipStreamSynchronize(m->st);
+        if (e == hipSuccess) e = hipStreamSynchronize(m->st);  // the staging buffer is reused next chunk
         if (e != hipSuccess) return m->ctx->hip_fail(e, "prefill");
         done += M;
     }
     m->len_h[slot] += n;
-    m->h_stage[0] = m->len_h[slot];
-    hipError_t e = hipMemcpyAsync(m->d_seq_len + slot, m->h_stage, 4, hipMemcpyHostToDevice, m->st);
-    if (e == hipSuccess) e = hipStreamSynchronize(m->st);
-    return e == hipSuccess ? BH_OK : m->ctx->hip_fail(e, "prefill");
+    return BH_OK;
+}
+
+// Device state of batch entry b: its slot, the first KV row of the slot's region, its next input
+// token and that token's position.
+static hipError_t set_entry(bh_model* m, int b, int slot, uint32_t token) {
+    const int32_t s32 = slot, t32 = (int32_t)token, p32 = m->len_h[slot];
+    const int64_t bo = m->off_h[slot];
+    hipError_t e = put(m, m->d_slot + b, &s32, 4);
+    if (e == hipSuccess) e = put(m, m->d_tok + b, &t32, 4);
+    if (e == hipSuccess) e = put(m, m->d_pos + b, &p32, 4);
+    if (e == hipSuccess) e = put(m, m->d_boff + b, &bo, 8);
+    return e;
 }
 
 int bh_model_decode_setup(bh_model* m, int batch, const int32_t* slots, const uint32_t* first_tokens) {
@@ -622,10 +672,11 @@ int bh_model_decode_setup(bh_model* m, int batch, const int32_t* slots, const ui
     if (batch != m->B) drop_graph(m);
     m->B = batch;
     m->bslots.assign(slots, slots + batch);
-    hipError_t e = hipMemcpyAsync(m->d_slot, slots, (size_t)batch * 4, hipMemcpyHostToDevice, m->st);
-    if (e == hipSuccess) e = hipMemcpyAsync(m->d_next, first_tokens, (size_t)batch * 4, hipMemcpyHostToDevice, m->st);
-    if (e == hipSuccess) e = hipStreamSynchronize(m->st);
-    return e == hipSuccess ? BH_OK : m->ctx->hip_fail(e, "decode_setup");
+    for (int b = 0; b < batch; ++b) {
+        hipError_t e = set_entry(m, b, slots[b], first_tokens[b]);
+        if (e != hipSuccess) return m->ctx->hip_fail(e, "decode_setup");
+    }
+    return BH_OK;
 }
 
 int bh_model_decode_replace(bh_model* m, int b, int slot, uint32_t first_token) {
@@ -636,11 +687,7 @@ int bh_model_decode_replace(bh_model* m, int b, int slot, uint32_t first_token) 
     for (int i = 0; i < m->B; ++i)
         if (i != b && m->bslots[i] == slot) return m->fail(BH_ERR_INVALID, "slot already in the batch");
     m->bslots[b] = slot;
-    m->h_stage[0] = slot;
-    m->h_stage[1] = (int32_t)first_token;
-    hipError_t e = hipMemcpyAsync(m->d_slot + b, &m->h_stage[0], 4, hipMemcpyHostToDevice, m->st);
-    if (e == hipSuccess) e = hipMemcpyAsync(m->d_next + b, &m->h_stage[1], 4, hipMemcpyHostToDevice, m->st);
-    if (e == hipSuccess) e = hipStreamSynchronize(m->st);
+    hipError_t e = set_entry(m, b, slot, first_token);
     return e == hipSuccess ? BH_OK : m->ctx->hip_fail(e, "decode_replace");
 }
 
@@ -673,7 +720,7 @@ static int decode_locked(bh_model* m, int n_steps, uint32_t* ids_out, float* raw
     int done = 0;
     while (done < n_steps && e == hipSuccess) {
         const int chunk = (int)std::min<int64_t>(n_steps - done, m->ids_steps);
-        e = launch_step_counter(m->d_step, 1, m->st);
+        e = decode_start(m);
         for (int s = 0; s < chunk && e == hipSuccess; ++s) {
             e = hipGraphLaunch(m->gexec, m->st);
             if (e == hipSuccess && raw_logits)
@@ -708,6 +755,13 @@ int bh_model_generate(bh_model* m, int slot, const uint32_t* prompt, int n_promp
     std::vector<uint32_t> toks(prompt, prompt + n_prompt);
     if (toks.empty()) toks.push_back(1);  // cpu_engine.rs:2487-2489
     const int64_t need = (int64_t)toks.size() + max_new;
+    for (int b = 0; b < m->B; ++b)
+        if (m->bslots[b] == slot) {  // a previous generate on this slot: leave the batch first
+            drop_graph(m);
+            m->B = 0;
+            m->bslots.clear();
+            break;
+        }
     int rc = bh_model_seq_open(m, slot, need);
     if (rc) return rc;
     rc = bh_model_prefill(m, slot, toks.data(), (int)toks.size() - 1);
@@ -749,7 +803,7 @@ int bh_model_time_kernels(bh_model* m, int n_steps, double* mean_us, int64_t* la
     attn_plan(decode_len_bound(m, n_steps), m->B, m->c.n_kv_heads, &splits, &rows);
     std::vector<double> tot(BH_K_COUNT, 0.0);
     std::vector<int64_t> cnt(BH_K_COUNT, 0);
-    hipError_t e = launch_step_counter(m->d_step, 1, m->st);
+    hipError_t e = decode_start(m);
     for (int s = 0; s < n_steps && e == hipSuccess; ++s) {
         m->timing = true;
         m->recs.clear();
@@ -759,7 +813,7 @@ int bh_model_time_kernels(bh_model* m, int n_steps, double* mean_us, int64_t* la
         if (e == hipSuccess) e = hipStreamSynchronize(m->st);
         for (auto& r : m->recs) {
             float ms = 0.f;
-            if (hipEventElapsedTime(&ms, r.a, r.b) == hipSuccess) {
+            if (hipEventElapsedTime(&ms, r.ev.start, r.ev.stop) == hipSuccess) {
                 tot[r.cls] += ms * 1000.0;
                 cnt[r.cls] += 1;
             }
@@ -778,18 +832,20 @@ int bh_model_kernel_bytes(bh_model* m, int kclass, double* bytes) {
     if (!m || !bytes) return BH_ERR_INVALID;
     const bh_model_config& c = m->c;
     const double B = m->B > 0 ? m->B : 1, H = c.hidden, I = c.ffn, QD = (double)m->QD, KD = (double)m->KD;
-    const double kvb = c.kv_f16 ? 2.0 : 4.0;
+    const double kvb = c.kv_f16 ? 2.0 : 4.0, T = m->ssq_tiles;
     const LayerW& w = m->L[0];
     switch (kclass) {
-        case BH_K_GEMV_QKV:
-            *bytes = weight_bytes(w.qkv) + (c.attn_bias ? (QD + 2 * KD) * 4 : 0) + B * H * 4 + B * QD * 4 +
+        case BH_K_GEMV_QKV:  // weights (+bias), xw and ssq in; q out, K/V rows appended
+            *bytes = weight_bytes(w.qkv) + (c.attn_bias ? (QD + 2 * KD) * 4 : 0) + B * (H + T) * 4 + B * QD * 4 +
                      B * 2 * KD * kvb;
             return BH_OK;
-        case BH_K_GEMV_O: *bytes = weight_bytes(w.o) + B * QD * 4 + 2 * B * H * 4; return BH_OK;
-        case BH_K_GEMV_GATEUP: *bytes = weight_bytes(w.gate) + weight_bytes(w.up) + B * H * 4 + B * I * 4; return BH_OK;
-        case BH_K_GEMV_DOWN: *bytes = weight_bytes(w.down) + B * I * 4 + 2 * B * H * 4; return BH_OK;
-        case BH_K_LM_HEAD:
-            *bytes = weight_bytes(m->embed) + B * H * 4 + B * (double)c.vocab * 4 + B * (double)c.vocab * 2;
+        case BH_K_GEMV_O:  // weights, attention out in; x read and written, xw and ssq out, norm weight
+            *bytes = weight_bytes(w.o) + B * QD * 4 + B * (3 * H + T) * 4 + H * 4;
+            return BH_OK;
+        case BH_K_GEMV_GATEUP: *bytes = weight_bytes(w.gate) + weight_bytes(w.up) + B * (H + T) * 4 + B * I * 4; return BH_OK;
+        case BH_K_GEMV_DOWN: *bytes = weight_bytes(w.down) + B * I * 4 + B * (3 * H + T) * 4 + H * 4; return BH_OK;
+        case BH_K_LM_HEAD:  // tied table, xw in; logits out, penalty counts read
+            *bytes = weight_bytes(m->embed) + B * (H + T) * 4 + B * (double)c.vocab * 4 + B * (double)c.vocab * 2;
             return BH_OK;
         case BH_K_ATTN: {
             double rows = 0;
@@ -801,7 +857,6 @@ int bh_model_kernel_bytes(bh_model* m, int kclass, double* bytes) {
             *bytes = rows * 2 * KD * kvb + 2 * B * QD * 4;
             return BH_OK;
         }
-        case BH_K_NORM: *bytes = 2 * B * H * 4 + H * 4; return BH_OK;
         default: *bytes = 0; return BH_OK;
     }
 }

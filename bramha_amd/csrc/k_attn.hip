@@ -4,16 +4,24 @@
 // per query head, online softmax over the cached rows of its KV head
 // (kv head = q head / (n_q / n_kv)), scores (q . k) * (1/sqrt(hd)), output o * (1/l).
 //
-// Design: one workgroup per (query row, KV head, context split). The G = n_q/n_kv
-// query heads that share a KV head are processed together, so every K/V byte is
-// read once per workgroup instead of once per query head (the reference re-reads
-// each KV head's rows G times). Each wavefront takes 64-row tiles and requests the
-// tile's K rows (lane t owns row t, 16-byte loads) and V rows (8 rows per step for
-// hd 64, 16-byte loads) together before computing: scores use q broadcast from LDS,
-// probabilities move between lanes with ds_bpermute. G is a compile-time constant
-// so all per-head state stays in registers. Splits of long contexts publish
-// (m, l, o) partials; the last workgroup of a (row, KV head) to finish merges them
-// with log-sum-exp weights (flash-decoding) — no second kernel.
+// Design: one workgroup per (query row, KV head, context split); the G = n_q/n_kv query heads
+// that share a KV head are processed together, so every K/V byte is read once per
+// workgroup instead of once per query head (the reference re-reads each KV head's rows G
+// times). Each wavefront takes 64-row tiles of the context.
+//
+// fp16 cache (k_attn_mf): both products run on MFMA (v_mfma_f32_16x16x32_f16) with the G
+// heads in the 16 columns. Scores S^T[t][h] = K[t][:] . Q[h][:] take K rows straight from the
+// cache (16-byte loads) and Q as fp16 hi + lo pairs (hi + lo carries ~22 bits of the f32 q);
+// the online softmax needs one max across the 4 row groups per tile and defers the sum to the
+// end; O^T[d][h] += V^T[d][t] . P^T[t][h] takes V^T from the transposed V cache (16-byte loads
+// of 8 consecutive rows of one column) and P as fp16 hi + lo. The K rows each lane loads are
+// permuted so that the probabilities a lane holds after the softmax are exactly the 8 rows its
+// P operand needs: no cross-lane data movement between the two products.
+// f32 cache (k_attn): VALU dot products with q broadcast from LDS and probabilities moved
+// between lanes with ds_bpermute.
+//
+// Splits of long contexts publish (m, l, o) partials; the last workgroup of a (row, KV head)
+// to finish merges them with log-sum-exp weights (flash-decoding) — no second kernel.
 #include "bh_internal.h"
 
 #include <hip/hip_fp16.h>
@@ -68,6 +76,39 @@ struct Row8 {
     }
 };
 
+// The last workgroup of a (row, KV head): log-sum-exp merge of the splits' (m, l, o) partials.
+template <int HD, int G>
+__device__ __forceinline__ void merge_splits(const AttnArgs& a, int64_t hq0) {
+    __shared__ float f_s[G][MAX_SPLITS];
+    __shared__ float L_s[G];
+    const int S = a.splits;
+    for (int i = threadIdx.x; i < G * S; i += blockDim.x) {
+        const int g = i / S, s2 = i % S;
+        f_s[g][s2] = a.part_ml[((hq0 + g) * S + s2) * 2];
+    }
+    __syncthreads();
+    if (threadIdx.x < G) {
+        const int g = threadIdx.x;
+        float M = -INFINITY;
+        for (int s2 = 0; s2 < S; ++s2) M = fmaxf(M, f_s[g][s2]);
+        float L = 0.f;
+        for (int s2 = 0; s2 < S; ++s2) {
+            const float ms = f_s[g][s2];
+            const float f = ms == -INFINITY ? 0.f : expf(ms - M);
+            L += a.part_ml[((hq0 + g) * S + s2) * 2 + 1] * f;
+            f_s[g][s2] = f;
+        }
+        L_s[g] = L;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < G * HD; i += blockDim.x) {
+        const int g = i / HD, d = i % HD;
+        float O = 0.f;
+        for (int s2 = 0; s2 < S; ++s2) O = fmaf(f_s[g][s2], a.part_o[((hq0 + g) * S + s2) * HD + d], O);
+        a.out[(hq0 + g) * HD + d] = O * (1.0f / L_s[g]);
+    }
+}
+
 template <int HD, int KVF16, int G>
 __global__ void __launch_bounds__(256) k_attn(const AttnArgs a) {
     constexpr int DL = HD / 8;   // lanes per row in the value phase
@@ -81,22 +122,24 @@ __global__ void __launch_bounds__(256) k_attn(const AttnArgs a) {
     const int b = blockIdx.z, h = blockIdx.y, sp = blockIdx.x;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 
-    int64_t off;
+    // q first: its address depends on nothing loaded
+    constexpr int QPT = (G * HD + 255) / 256;
+    float qreg[QPT];
+#pragma unroll
+    for (int k = 0; k < QPT; ++k) {
+        const int i = threadIdx.x + k * 256;
+        qreg[k] = i < G * HD ? a.q[((int64_t)b * a.nq + h * G) * HD + i] : 0.f;
+    }
+    const int64_t off = a.boff[b];
     int len;
     if (a.seq_len) {
-        off = a.seq_off[b];
         len = a.seq_len[b];
     } else {
-        off = a.seq_off[a.slot[b]];
         len = a.pos[b] + 1;
         if (a.kv.max_context > 0) len = min(len, a.kv.max_context);
     }
     const int r0 = sp * a.split_rows;
     const int r1 = min(len, r0 + a.split_rows);
-
-    for (int i = threadIdx.x; i < G * HD; i += blockDim.x)
-        q_s[i / HD][i % HD] = a.q[((int64_t)b * a.nq + h * G) * HD + i];
-    __syncthreads();
 
     const float scale = 1.0f / sqrtf((float)HD);
     const int64_t kv_base = ((int64_t)h * a.kv.kv_rows + off) * HD;
@@ -109,15 +152,13 @@ __global__ void __launch_bounds__(256) k_attn(const AttnArgs a) {
         for (int e = 0; e < 8; ++e) o[g][e] = 0.f;
     }
     const int tsub = lane / DL, dl = lane % DL;
-
-    for (int t0 = r0 + wave * 64; t0 < r1; t0 += 4 * 64) {
+    // K rows (lane t owns row t) and V rows (TS rows per step) of a 64-row tile, requested together
+    Row8<KVF16> kr[HD / 8], vr[NV];
+    auto load_tile = [&](int t0) {
         const int t = t0 + lane;
-        const bool valid = t < r1;
-        // request the tile's K and V rows together
-        Row8<KVF16> kr[HD / 8], vr[NV];
 #pragma unroll
         for (int dc = 0; dc < HD / 8; ++dc) {
-            if (valid) kr[dc].load(a.kv.k, kv_base + (int64_t)t * HD + dc * 8);
+            if (t < r1) kr[dc].load(a.kv.k, kv_base + (int64_t)t * HD + dc * 8);
             else kr[dc].zero();
         }
 #pragma unroll
@@ -126,6 +167,19 @@ __global__ void __launch_bounds__(256) k_attn(const AttnArgs a) {
             if (t2 < r1) vr[j].load(a.kv.v, kv_base + (int64_t)t2 * HD + dl * 8);
             else vr[j].zero();
         }
+    };
+    const int tfirst = r0 + wave * 64;
+    if (tfirst < r1) load_tile(tfirst);
+#pragma unroll
+    for (int k = 0; k < QPT; ++k) {
+        const int i = threadIdx.x + k * 256;
+        if (i < G * HD) q_s[i / HD][i % HD] = qreg[k];
+    }
+    __syncthreads();
+
+    for (int t0 = tfirst; t0 < r1; t0 += 4 * 64) {
+        if (t0 != tfirst) load_tile(t0);
+        const bool valid = t0 + lane < r1;
         float s[G];
 #pragma unroll
         for (int g = 0; g < G; ++g) s[g] = 0.f;
@@ -151,7 +205,7 @@ __global__ void __launch_bounds__(256) k_attn(const AttnArgs a) {
             // keep the q reads of later chunks from being hoisted into registers
             __builtin_amdgcn_sched_barrier(0);
         }
-        float pg[G];
+    float pg[G];
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             const float sc = valid ? s[g] * scale : -INFINITY;
@@ -233,40 +287,218 @@ __global__ void __launch_bounds__(256) k_attn(const AttnArgs a) {
     __syncthreads();
     if (!s_last) return;
     __threadfence();
-    __shared__ float f_s[G][MAX_SPLITS];
-    __shared__ float L_s[G];
-    const int S = a.splits;
-    for (int i = threadIdx.x; i < G * S; i += blockDim.x) {
-        const int g = i / S, s2 = i % S;
-        f_s[g][s2] = a.part_ml[((hq0 + g) * S + s2) * 2];
+    merge_splits<HD, G>(a, hq0);
+    if (threadIdx.x == 0) a.cnt[b * a.nkv + h] = 0;  // ready for the next launch
+}
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// f32 x[0..7] -> fp16 hi and lo with hi + lo == x to ~22 bits
+__device__ __forceinline__ void split_hl(const float* x, half8& hi, half8& lo) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        const _Float16 h = (_Float16)x[s];
+        hi[s] = h;
+        lo[s] = (_Float16)(x[s] - (float)h);
     }
-    __syncthreads();
-    if (threadIdx.x < G) {
-        const int g = threadIdx.x;
-        float M = -INFINITY;
-        for (int s2 = 0; s2 < S; ++s2) M = fmaxf(M, f_s[g][s2]);
-        float L = 0.f;
-        for (int s2 = 0; s2 < S; ++s2) {
-            const float ms = f_s[g][s2];
-            const float f = ms == -INFINITY ? 0.f : expf(ms - M);
-            L += a.part_ml[((hq0 + g) * S + s2) * 2 + 1] * f;
-            f_s[g][s2] = f;
+}
+
+// Row of the 64-row tile that lane-group row i of 16-row block blk holds: block pairs (2j, 2j+1)
+// cover rows 32j .. 32j+31 with row group g = i / 4 owning rows 32j + 8g .. 32j + 8g + 7.
+__device__ __forceinline__ int mf_row(int blk, int i) { return 32 * (blk >> 1) + 8 * (i >> 2) + 4 * (blk & 1) + (i & 3); }
+
+template <int HD, int G>
+__global__ void __launch_bounds__(256) k_attn_mf(const AttnArgs a) {
+    constexpr int KC = HD / 32;  // 32-wide head-dim chunks of the score product
+    constexpr int DB = HD / 16;  // 16-wide head-dim blocks of the value product
+    __shared__ float q_s[16][HD];
+    __shared__ float w_m[4][16], w_l[4][16];
+    __shared__ float w_o[4][16][HD + 4];
+    __shared__ int s_last;
+
+    const int b = blockIdx.z, h = blockIdx.y, sp = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lr = lane & 15, lg = lane >> 4;
+
+    // q first: its address depends on nothing loaded
+    constexpr int QPT = 16 * HD / 256;
+    float qreg[QPT];
+#pragma unroll
+    for (int k = 0; k < QPT; ++k) {
+        const int i = threadIdx.x + k * 256;
+        qreg[k] = i / HD < G ? a.q[((int64_t)b * a.nq + h * G) * HD + i] : 0.f;
+    }
+    const int64_t off = a.boff[b];
+    int len;
+    if (a.seq_len) {
+        len = a.seq_len[b];
+    } else {
+        len = a.pos[b] + 1;
+        if (a.kv.max_context > 0) len = min(len, a.kv.max_context);
+    }
+    const int r0 = sp * a.split_rows;
+    const int r1 = min(len, r0 + a.split_rows);
+    const __half* Kc = (const __half*)a.kv.k + ((int64_t)h * a.kv.kv_rows + off) * HD;
+    const __half* Vt = (const __half*)a.kv.v + (int64_t)h * HD * a.kv.kv_rows + off;  // + d * kv_rows + t
+    const bool v_aligned = ((off | a.kv.kv_rows) & 7) == 0;
+
+    half8 kf[4][KC], vf[2][DB];
+    auto load_tile = [&](int t0) {
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk) {
+            const int t = t0 + mf_row(blk, lr);
+#pragma unroll
+            for (int kc = 0; kc < KC; ++kc) {
+                if (t < r1) kf[blk][kc] = *(const half8*)(Kc + (int64_t)t * HD + kc * 32 + 8 * lg);
+                else kf[blk][kc] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+            }
         }
-        L_s[g] = L;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int tg = t0 + 32 * j + 8 * lg;  // this lane group's 8 rows
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                const __half* p = Vt + (int64_t)(db * 16 + lr) * a.kv.kv_rows + tg;
+                if (v_aligned && tg + 7 < r1) {
+                    vf[j][db] = *(const half8*)p;
+                } else {
+                    half8 v;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[e] = tg + e < r1 ? (_Float16)__half2float(p[e]) : (_Float16)0.f;
+                    vf[j][db] = v;
+                }
+            }
+        }
+    };
+    const int tfirst = r0 + wave * 64;
+    if (tfirst < r1) load_tile(tfirst);
+#pragma unroll
+    for (int k = 0; k < QPT; ++k) {
+        const int i = threadIdx.x + k * 256;
+        q_s[i / HD][i % HD] = qreg[k];
     }
     __syncthreads();
+    // Q^T as the B operand: lane (lr, lg) holds head lr, head-dim kc*32 + 8lg .. +7
+    half8 qh[KC], ql[KC];
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) split_hl(&q_s[lr][kc * 32 + 8 * lg], qh[kc], ql[kc]);
+
+    const float scale = 1.0f / sqrtf((float)HD);
+    float m = -INFINITY, l = 0.f;  // head lr: running max; this lane's share of the sum
+    f32x4 o[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int t0 = tfirst; t0 < r1; t0 += 4 * 64) {
+        if (t0 != tfirst) load_tile(t0);
+        // S^T: lane holds rows mf_row(blk, 4lg + v) of head lr
+        f32x4 sc[4];
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kc = 0; kc < KC; ++kc) {
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[blk][kc], qh[kc], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[blk][kc], ql[kc], acc, 0, 0, 0);
+            }
+            sc[blk] = acc;
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const bool ok = t0 + mf_row(blk, 4 * lg + v) < r1;
+                sc[blk][v] = ok ? sc[blk][v] * scale : -INFINITY;
+                tmax = fmaxf(tmax, sc[blk][v]);
+            }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float mn = fmaxf(m, tmax);
+        const float alpha = m == -INFINITY ? 0.f : expf(m - mn);
+        m = mn;
+        float ps = 0.f;
+        float pr[4][4];
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float p = sc[blk][v] == -INFINITY ? 0.f : expf(sc[blk][v] - mn);
+                pr[blk][v] = p;
+                ps += p;
+            }
+        l = l * alpha + ps;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) o[db] *= alpha;
+        // O^T += V^T . P^T over rows 32j .. 32j+31: the lane's P slots s = 0..3 are block 2j,
+        // s = 4..7 block 2j+1 — rows 32j + 8lg + s, the rows of its V^T operand
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            float pv[8];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                pv[v] = pr[2 * j][v];
+                pv[4 + v] = pr[2 * j + 1][v];
+            }
+            half8 ph, pl;
+            split_hl(pv, ph, pl);
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[j][db], ph, o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[j][db], pl, o[db], 0, 0, 0);
+            }
+        }
+    }
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if (lg == 0) {
+        w_m[wave][lr] = m;
+        w_l[wave][lr] = l;
+    }
+    // O^T D layout: lane holds head lr, head-dim db*16 + 4lg + v
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) w_o[wave][lr][db * 16 + 4 * lg + v] = o[db][v];
+    __syncthreads();
+
+    const int64_t hq0 = (int64_t)b * a.nq + h * G;
     for (int i = threadIdx.x; i < G * HD; i += blockDim.x) {
         const int g = i / HD, d = i % HD;
-        float O = 0.f;
-        for (int s2 = 0; s2 < S; ++s2) O = fmaf(f_s[g][s2], a.part_o[((hq0 + g) * S + s2) * HD + d], O);
-        a.out[(hq0 + g) * HD + d] = O * (1.0f / L_s[g]);
+        float M = -INFINITY;
+        for (int w = 0; w < 4; ++w) M = fmaxf(M, w_m[w][g]);
+        float L = 0.f, O = 0.f;
+        for (int w = 0; w < 4; ++w) {
+            const float f = w_m[w][g] == -INFINITY ? 0.f : expf(w_m[w][g] - M);
+            L += w_l[w][g] * f;
+            O += w_o[w][g][d] * f;
+        }
+        if (a.splits == 1) {
+            a.out[(hq0 + g) * HD + d] = O * (1.0f / L);
+        } else {
+            a.part_o[((hq0 + g) * a.splits + sp) * HD + d] = O;
+            if (d == 0) {
+                a.part_ml[((hq0 + g) * a.splits + sp) * 2] = M;
+                a.part_ml[((hq0 + g) * a.splits + sp) * 2 + 1] = L;
+            }
+        }
     }
+    if (a.splits == 1) return;
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) s_last = atomicAdd(&a.cnt[b * a.nkv + h], 1) == a.splits - 1;
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    merge_splits<HD, G>(a, hq0);
     if (threadIdx.x == 0) a.cnt[b * a.nkv + h] = 0;  // ready for the next launch
 }
 
 template <int HD, int KVF16, int G>
 hipError_t launch_t(const AttnArgs& a, hipStream_t st) {
-    hipLaunchKernelGGL((k_attn<HD, KVF16, G>), dim3(a.splits, a.nkv, a.batch), dim3(256), 0, st, a);
+    if constexpr (KVF16) launch_kernel((k_attn_mf<HD, G>), dim3(a.splits, a.nkv, a.batch), dim3(256), 0, st, a);
+    else launch_kernel((k_attn<HD, 0, G>), dim3(a.splits, a.nkv, a.batch), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 
@@ -284,12 +516,14 @@ hipError_t launch_g(const AttnArgs& a, hipStream_t st) {
 
 }  // namespace
 
-// Context split: 256 rows per workgroup (one 64-row tile per wave); 64 when that leaves
-// fewer than 256 workgroups; at most 128 splits (longer splits loop over tiles).
+// Context split: 256 rows per workgroup (one 64-row tile per wave). Contexts up to 512 rows
+// stay in one workgroup per (row, KV head) — its waves loop over at most two tiles, cheaper
+// than the cross-workgroup merge; at most 128 splits (longer splits loop over tiles).
 void attn_plan(int max_len, int batch, int nkv, int* splits, int* split_rows) {
+    (void)batch;
+    (void)nkv;
     max_len = std::max(max_len, 1);
-    int rows = 256;
-    if ((int64_t)((max_len + 255) / 256) * nkv * batch < 256) rows = 64;
+    int rows = max_len <= 512 ? 512 : 256;
     int s = (max_len + rows - 1) / rows;
     if (s > MAX_SPLITS) {
         rows = ((max_len + MAX_SPLITS - 1) / MAX_SPLITS + 255) / 256 * 256;

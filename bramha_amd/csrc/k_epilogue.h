@@ -1,9 +1,9 @@
 // k_epilogue.h — epilogues shared by the GEMV and MFMA GEMM kernels.
 //
 // Input: fin[(j * B + b) * ROWS + r] holds the finished sums (unscaled for the row formats)
-// of weight j (gate/up pair: j = 0, 1), batch row b, weight row row0 + r; kws is the
-// workgroup's K split (EPI_PART). `scratch` has room for B * ROWS floats. All threads
-// of the workgroup call it.
+// of weight j (gate/up pair: j = 0, 1), batch row b, weight row row0 + r. rn[b] is the
+// token's RMSNorm factor when the activations are a normalized residual stream (else 1).
+// `scratch` has room for B * ROWS floats. All threads of the workgroup call it.
 #pragma once
 
 #include <hip/hip_fp16.h>
@@ -32,39 +32,67 @@ __device__ __forceinline__ void argmax_combine(float& v, int& i, float ov, int o
     }
 }
 
+__device__ __forceinline__ float wave_sum64(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+// rnorm of the residual stream for row b: 1/sqrt(sum_t ssq[b][t] / n + eps), the tiles summed in
+// order (rms_norm_into, cpu_engine.rs:1292-1302, with the sum of squares computed per tile).
+__device__ __forceinline__ float stream_rnorm(const GemvArgs& a, int b) {
+    const float* s = a.ssq_in + (int64_t)b * a.ssq_tiles;
+    float t = 0.f;
+    for (int i = 0; i < a.ssq_tiles; ++i) t += s[i];
+    return 1.0f / sqrtf(t / a.norm_n + a.eps);
+}
 
 template <int FMT, int B, int EPI, int ROWS>
-__device__ __forceinline__ void run_epilogue(const GemvArgs& a, const float* fin, float* scratch, int64_t row0,
-                                             int kws) {
+__device__ __forceinline__ void run_epilogue(const GemvArgs& a, const float* fin, float* scratch, const float* rn,
+                                             int64_t row0) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int nwaves = blockDim.x >> 6;
-    if constexpr (EPI == EPI_PART) {
-        float* part = a.part + (int64_t)kws * a.part_ld;
+    if constexpr (EPI == EPI_STORE) {
         for (int i = threadIdx.x; i < B * ROWS; i += blockDim.x) {
             const int b = i / ROWS, rr = i % ROWS;
             const int64_t nn = row0 + rr;
             if (nn >= a.N || b >= a.batch) continue;
-            part[(int64_t)b * a.N + nn] = fin[i] * row_scale<FMT>(a.S, nn);
-        }
-    } else if constexpr (EPI == EPI_STORE || EPI == EPI_RESID) {
-        for (int i = threadIdx.x; i < B * ROWS; i += blockDim.x) {
-            const int b = i / ROWS, rr = i % ROWS;
-            const int64_t nn = row0 + rr;
-            if (nn >= a.N || b >= a.batch) continue;
-            float v = fin[i] * row_scale<FMT>(a.S, nn);
+            float v = fin[i] * row_scale<FMT>(a.S, nn) * rn[b];
             if (a.bias) v += a.bias[nn];
-            float* yp = a.y + (int64_t)b * a.ldy + nn;
-            if constexpr (EPI == EPI_RESID) *yp = *yp + v;
-            else *yp = v;
+            a.y[(int64_t)b * a.ldy + nn] = v;
+        }
+    } else if constexpr (EPI == EPI_RESNORM) {
+        // residual add (cpu_engine.rs:2937-2939, 2966-2968), then the next norm's inputs
+        static_assert(ROWS == 64, "one sum of squares per 64-row tile");
+        for (int i = threadIdx.x; i < B * ROWS; i += blockDim.x) {
+            const int b = i / ROWS, rr = i % ROWS;
+            const int64_t nn = row0 + rr;
+            float sq = 0.f;
+            if (nn < a.N && b < a.batch) {
+                float o = fin[i] * row_scale<FMT>(a.S, nn);
+                if (a.bias) o += a.bias[nn];
+                float* xp = a.y + (int64_t)b * a.ldy + nn;
+                const float v = *xp + o;
+                *xp = v;
+                a.xw_out[(int64_t)b * a.ldy + nn] = v * a.wnext[nn];
+                sq = v * v;
+            }
+            scratch[i] = sq;
+        }
+        __syncthreads();
+        const int64_t tile = row0 / 64;
+        for (int b = wave; b < B; b += nwaves) {
+            const float t = wave_sum64(scratch[b * ROWS + lane]);
+            if (lane == 0 && b < a.batch) a.ssq_out[(int64_t)b * a.ssq_tiles + tile] = t;
         }
     } else if constexpr (EPI == EPI_SILU) {
         for (int i = threadIdx.x; i < B * ROWS; i += blockDim.x) {
             const int b = i / ROWS, rr = i % ROWS;
             const int64_t nn = row0 + rr;
             if (nn >= a.N || b >= a.batch) continue;
-            const float g = fin[i] * row_scale<FMT>(a.S, nn);
-            const float u = fin[B * ROWS + i] * row_scale<FMT>(a.S2, nn);
+            const float g = fin[i] * row_scale<FMT>(a.S, nn) * rn[b];
+            const float u = fin[B * ROWS + i] * row_scale<FMT>(a.S2, nn) * rn[b];
             a.y[(int64_t)b * a.ldy + nn] = g * (1.0f / (1.0f + expf(-g))) * u;
         }
     } else if constexpr (EPI == EPI_QKV) {
@@ -73,7 +101,7 @@ __device__ __forceinline__ void run_epilogue(const GemvArgs& a, const float* fin
             const int b = i / ROWS, rr = i % ROWS;
             const int64_t nn = row0 + rr;
             if (nn >= a.N || b >= a.batch) continue;
-            float val = fin[i] * row_scale<FMT>(a.S, nn);
+            float val = fin[i] * row_scale<FMT>(a.S, nn) * rn[b];
             if (a.bias) val += a.bias[nn];
             const int sec = nn < a.qd ? 0 : (nn < a.qd + a.kd ? 1 : 2);
             const int loc = (int)nn - (sec == 0 ? 0 : (sec == 1 ? a.qd : a.qd + a.kd));
@@ -81,7 +109,7 @@ __device__ __forceinline__ void run_epilogue(const GemvArgs& a, const float* fin
             const int p = a.pos[b];
             if (sec < 2) {  // rotate-half RoPE (apply_rope_cpu, cpu_engine.rs:1682-1699)
                 const int dp = d < half ? half : -half;
-                float pv = fin[i + dp] * row_scale<FMT>(a.S, nn + dp);
+                float pv = fin[i + dp] * row_scale<FMT>(a.S, nn + dp) * rn[b];
                 if (a.bias) pv += a.bias[nn + dp];
                 const float2 cs = a.rope[(int64_t)p * half + (d < half ? d : d - half)];
                 val = d < half ? (val * cs.x - pv * cs.y) : (val * cs.x + pv * cs.y);
@@ -89,11 +117,15 @@ __device__ __forceinline__ void run_epilogue(const GemvArgs& a, const float* fin
             if (sec == 0) {
                 a.y[(int64_t)b * a.ldy + nn] = val;
             } else {
-                const int64_t row = a.seq_off[a.slot[b]] + kv_phys_row(a.kv, p);
-                const int64_t off = ((int64_t)hh * a.kv.kv_rows + row) * a.hd + d;
-                void* base = sec == 1 ? a.kv.k : a.kv.v;
-                if (a.kv.kv_f16) ((__half*)base)[off] = __float2half(val);
-                else ((float*)base)[off] = val;
+                const int64_t row = a.boff[b] + kv_phys_row(a.kv, p);
+                if (sec == 2 && a.kv.kv_f16) {  // fp16 V is stored transposed
+                    ((__half*)a.kv.v)[((int64_t)hh * a.hd + d) * a.kv.kv_rows + row] = __float2half(val);
+                } else {
+                    const int64_t off = ((int64_t)hh * a.kv.kv_rows + row) * a.hd + d;
+                    void* base = sec == 1 ? a.kv.k : a.kv.v;
+                    if (a.kv.kv_f16) ((__half*)base)[off] = __float2half(val);
+                    else ((float*)base)[off] = val;
+                }
             }
         }
     } else if constexpr (EPI == EPI_LMHEAD) {
@@ -103,7 +135,7 @@ __device__ __forceinline__ void run_epilogue(const GemvArgs& a, const float* fin
             const int64_t nn = row0 + rr;
             float pv = -INFINITY;
             if (nn < a.N && b < a.batch) {
-                float v = fin[i] * row_scale<FMT>(a.S, nn);
+                float v = fin[i] * row_scale<FMT>(a.S, nn) * rn[b];
                 a.y[(int64_t)b * a.ldy + nn] = v;
                 const int cnt = a.pen[(int64_t)a.slot[b] * a.vocab + nn];
                 for (int t = 0; t < cnt; ++t) v = v > 0.f ? v / 1.15f : v * 1.15f;

@@ -32,54 +32,6 @@ __global__ void __launch_bounds__(256) k_rmsnorm(const float* __restrict__ x, co
     for (int i = threadIdx.x; i < n; i += blockDim.x) orow[i] = xr[i] * scale * w[i];
 }
 
-// The residual add of the O / down projection (cpu_engine.rs:2937-2939, 2966-2968)
-// followed by the next RMSNorm (rms_norm_into, :1292-1302), one workgroup per row:
-// o = sum of the projection's split-K partial sums in split order (+ bias), x += o,
-// h = x * (1/sqrt(mean(x^2) + eps)) * w. Holds up to 16 elements per thread (n <= 4096).
-__global__ void __launch_bounds__(256) k_resid_norm(float* __restrict__ x, const float* __restrict__ part,
-                                                    int splits, int64_t part_ld, const float* __restrict__ bias,
-                                                    const float* __restrict__ w, float eps, float* __restrict__ h,
-                                                    int n) {
-    __shared__ float red[16];
-    constexpr int MAXJ = 16;
-    const int b = blockIdx.x;
-    float* xr = x + (int64_t)b * n;
-    float v[MAXJ];
-    float ss = 0.f;
-#pragma unroll
-    for (int j = 0; j < MAXJ; ++j) {
-        const int i = threadIdx.x + j * blockDim.x;
-        v[j] = 0.f;
-        if (i < n) {
-            float t = xr[i];
-            if (splits > 0) {
-                // all (up to 16) partial loads in flight at once: the index is clamped so
-                // every load is in bounds, the add is masked past `splits`
-                const float* pp = part + (int64_t)b * n + i;
-                float pv[16];
-#pragma unroll
-                for (int s = 0; s < 16; ++s) pv[s] = pp[(int64_t)min(s, splits - 1) * part_ld];
-                float o = 0.f;
-#pragma unroll
-                for (int s = 0; s < 16; ++s) o += s < splits ? pv[s] : 0.f;
-                if (bias) o += bias[i];
-                t = t + o;
-                xr[i] = t;
-            }
-            v[j] = t;
-            ss += t * t;
-        }
-    }
-    ss = block_sum(ss, red);
-    const float scale = 1.0f / sqrtf(ss / (float)n + eps);
-    float* hr = h + (int64_t)b * n;
-#pragma unroll
-    for (int j = 0; j < MAXJ; ++j) {
-        const int i = threadIdx.x + j * blockDim.x;
-        if (i < n) hr[i] = v[j] * scale * w[i];
-    }
-}
-
 // apply_rope_cpu (cpu_engine.rs:1682-1699) with a host-computed (cos, sin) table.
 __global__ void k_rope(float* __restrict__ v, const int32_t* __restrict__ pos, const float2* __restrict__ tab,
                        int n_heads, int hd) {
@@ -133,61 +85,62 @@ __global__ void k_dequant(int fmt, const uint4* __restrict__ Q, const void* __re
     }
 }
 
-// Embedding row copy (cpu_engine.rs:2820-2825, id % vocab) from the tied table in KM16
-// layout. With the decode prologue, the token comes from the previous step's argmax
-// and the position from the sequence's row count, which advances by one.
-__global__ void __launch_bounds__(256) k_embed(int fmt, const uint4* __restrict__ Q, const __half* __restrict__ S,
-                                               int64_t vocab, int64_t n_pad, int hidden, int32_t* tok, int32_t* pos,
-                                               const int32_t* slot, int32_t* seq_len, const uint32_t* next,
-                                               int prologue, float* x, int64_t ldx) {
-    __shared__ int32_t s_tok;
-    const int b = blockIdx.x;
-    if (threadIdx.x == 0) {
-        int32_t t;
-        if (prologue) {
-            t = (int32_t)next[b];
-            tok[b] = t;
-            const int s = slot[b];
-            const int32_t p = seq_len[s];
-            pos[b] = p;
-            seq_len[s] = p + 1;
-        } else {
-            t = tok[b];
+// Element i of row `id` of the tied embedding table in KM16 layout (F32 or Q4_G32):
+// the embedding row copy of cpu_engine.rs:2820-2825, dequantized bit-exactly like
+// dequantize_int4 (quantization.rs:102-122) with the group's fp16 scale.
+__device__ __forceinline__ float embed_elem(const DevWeight& t, int64_t id, int i) {
+    const int64_t c = t.fmt == BH_F32 ? (i >> 2) : (i >> 5);
+    if (t.fmt == BH_F32) return ((const float*)t.q)[(c * t.n_pad + id) * 4 + (i & 3)];
+    const uint8_t byte = ((const uint8_t*)t.q)[(c * t.n_pad + id) * 16 + ((i & 31) >> 1)];
+    const float nib = (i & 1) ? (float)(byte & 0x0F) : (float)((byte >> 4) & 0x0F);
+    return (nib - 8.0f) * __half2float(((const __half*)t.s)[c * t.n_pad + id]);
+}
+
+// Residual stream of token row b from embedding row `id`: x, xw = x * w0, and per-64-element
+// sums of squares (one wave per tile, a fixed shuffle order).
+__device__ __forceinline__ void embed_stream(const DevWeight& t, int64_t id, const float* w0, float* x, float* xw,
+                                             float* ssq, int ssq_tiles, int b) {
+    const int hidden = (int)t.k;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    float* xr = x + (int64_t)b * hidden;
+    float* xwr = xw + (int64_t)b * hidden;
+    for (int tl = wave; tl < ssq_tiles; tl += nw) {
+        const int i = tl * 64 + lane;
+        float v = 0.f;
+        if (i < hidden) {
+            v = embed_elem(t, id, i);
+            xr[i] = v;
+            xwr[i] = v * w0[i];
         }
-        s_tok = t;
-    }
-    __syncthreads();
-    const int64_t id = (int64_t)((uint32_t)s_tok % (uint64_t)vocab);
-    float* xr = x + (int64_t)b * ldx;
-    if (fmt == BH_F32) {
-        const float* F = (const float*)Q;
-        for (int i = threadIdx.x; i < hidden; i += blockDim.x) xr[i] = F[((int64_t)(i >> 2) * n_pad + id) * 4 + (i & 3)];
-    } else {
-        const uint8_t* B8 = (const uint8_t*)Q;
-        for (int i = threadIdx.x; i < hidden; i += blockDim.x) {
-            const int64_t c = i >> 5;
-            const uint8_t byte = B8[(c * n_pad + id) * 16 + ((i & 31) >> 1)];
-            const float nib = (i & 1) ? (float)(byte & 0x0F) : (float)((byte >> 4) & 0x0F);
-            xr[i] = (nib - 8.0f) * __half2float(S[c * n_pad + id]);
-        }
+        float sq = v * v;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
+        if (lane == 0) ssq[(int64_t)b * ssq_tiles + tl] = sq;
     }
 }
 
-// Final first-max argmax over the LM head's per-tile partials (cpu_engine.rs:3024-3031);
-// bumps the sequence's penalty count for the chosen id and records it.
-__global__ void __launch_bounds__(256) k_sample_final(const float* __restrict__ pv, const int32_t* __restrict__ pi,
-                                                      int tiles, const int32_t* slot, uint16_t* pen, int vocab,
-                                                      uint32_t* next, uint32_t* ids_cap, int32_t* step_ctr,
-                                                      int batch) {
+__global__ void __launch_bounds__(256) k_embed(const DevWeight t, const int32_t* __restrict__ tok,
+                                               const float* __restrict__ w0, float* x, float* xw, float* ssq,
+                                               int ssq_tiles, int32_t* reset_step) {
+    const int b = blockIdx.x;
+    const int64_t id = (int64_t)((uint32_t)tok[b] % (uint64_t)t.n);
+    if (reset_step && threadIdx.x == 0) reset_step[b] = 0;
+    embed_stream(t, id, w0, x, xw, ssq, ssq_tiles, b);
+}
+
+// End of a decode step for batch entry b = blockIdx.x: the first-max argmax over the LM head's
+// per-tile partials (cpu_engine.rs:3024-3031; ties keep the lowest id), the penalty count of the
+// chosen id, the id capture, the next token and position, and the next step's residual stream.
+__global__ void __launch_bounds__(256) k_sample(const SampleArgs a, const DevWeight t) {
     __shared__ float sv[4];
     __shared__ int si[4];
+    __shared__ int s_id;
     const int b = blockIdx.x;
-    const int step = step_ctr ? step_ctr[0] : 0;
     float v = -INFINITY;
     int idx = 0x7fffffff;
-    for (int t = threadIdx.x; t < tiles; t += blockDim.x) {
-        const float ov = pv[(int64_t)b * tiles + t];
-        const int oi = pi[(int64_t)b * tiles + t];
+    for (int i = threadIdx.x; i < a.tiles; i += blockDim.x) {
+        const float ov = a.part_val[(int64_t)b * a.tiles + i];
+        const int oi = a.part_idx[(int64_t)b * a.tiles + i];
         if (ov > v || (ov == v && oi < idx)) {
             v = ov;
             idx = oi;
@@ -215,64 +168,58 @@ __global__ void __launch_bounds__(256) k_sample_final(const float* __restrict__ 
                 idx = si[w];
             }
         if (idx == 0x7fffffff) idx = 0;  // no finite logit: the scan keeps index 0
-        next[b] = (uint32_t)idx;
-        uint16_t* c = pen + (int64_t)slot[b] * vocab + idx;
+        uint16_t* c = a.pen + (int64_t)a.slot[b] * a.vocab + idx;
         if (*c < 0xFFFF) *c = *c + 1;
-        if (ids_cap) ids_cap[(int64_t)step * batch + b] = (uint32_t)idx;
+        if (a.ids_cap) {
+            const int s = a.step[b];
+            a.ids_cap[(int64_t)s * a.batch + b] = (uint32_t)idx;
+            a.step[b] = s + 1;
+        }
+        a.tok[b] = idx;
+        a.pos[b] = a.pos[b] + 1;
+        s_id = idx;
     }
+    __syncthreads();
+    embed_stream(t, s_id, a.w0, a.x, a.xw, a.ssq, a.ssq_tiles, b);
 }
-
-__global__ void k_step_counter(int32_t* ctr, int reset) { ctr[0] = reset ? 0 : ctr[0] + 1; }
 
 }  // namespace
 
 hipError_t launch_rmsnorm(const float* x, const float* w, float eps, float* out, int rows, int n, hipStream_t st) {
-    hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(256), 0, st, x, w, eps, out, n);
-    return hipGetLastError();
-}
-
-hipError_t launch_resid_norm(float* x, const float* part, int splits, int64_t part_ld, const float* bias,
-                             const float* w, float eps, float* h, int rows, int n, hipStream_t st) {
-    if (n > 16 * 256 || splits > 16) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_resid_norm, dim3(rows), dim3(256), 0, st, x, part, splits, part_ld, bias, w, eps, h, n);
+    launch_kernel(k_rmsnorm, dim3(rows), dim3(256), 0, st, x, w, eps, out, n);
     return hipGetLastError();
 }
 
 hipError_t launch_rope(float* v, const int32_t* pos, const float2* tab, int rows, int n_heads, int hd, hipStream_t st) {
-    hipLaunchKernelGGL(k_rope, dim3(rows), dim3(256), 0, st, v, pos, tab, n_heads, hd);
+    launch_kernel(k_rope, dim3(rows), dim3(256), 0, st, v, pos, tab, n_heads, hd);
     return hipGetLastError();
 }
 
 hipError_t launch_silu_mul(const float* g, const float* u, float* out, int64_t n, hipStream_t st) {
     const int64_t blocks = std::min<int64_t>((n + 255) / 256, 4096);
-    hipLaunchKernelGGL(k_silu_mul, dim3((unsigned)std::max<int64_t>(blocks, 1)), dim3(256), 0, st, g, u, out, n);
+    launch_kernel(k_silu_mul, dim3((unsigned)std::max<int64_t>(blocks, 1)), dim3(256), 0, st, g, u, out, n);
     return hipGetLastError();
 }
 
 hipError_t launch_dequant(const DevWeight& w, float* out, hipStream_t st) {
     const int64_t total = w.n * w.chunks;
-    hipLaunchKernelGGL(k_dequant, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, w.fmt, (const uint4*)w.q,
+    launch_kernel(k_dequant, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, w.fmt, (const uint4*)w.q,
                        w.s, w.n, w.k, w.n_pad, w.chunks, out);
     return hipGetLastError();
 }
 
-hipError_t launch_embed(const DevWeight& t, int32_t* tok, int32_t* pos, const int32_t* slot, int32_t* seq_len,
-                        const uint32_t* next, int prologue, float* x, int64_t ldx, int batch, hipStream_t st) {
-    hipLaunchKernelGGL(k_embed, dim3(batch), dim3(256), 0, st, t.fmt, (const uint4*)t.q, (const __half*)t.s, t.n,
-                       t.n_pad, (int)t.k, tok, pos, slot, seq_len, next, prologue, x, ldx);
+hipError_t launch_embed(const DevWeight& t, const int32_t* tok, const float* w0, float* x, float* xw, float* ssq,
+                        int ssq_tiles, int32_t* reset_step, int batch, hipStream_t st) {
+    if (batch <= 0) return hipSuccess;
+    if (ssq_tiles != (int)((t.k + 63) / 64)) return hipErrorInvalidValue;
+    launch_kernel(k_embed, dim3(batch), dim3(256), 0, st, t, tok, w0, x, xw, ssq, ssq_tiles, reset_step);
     return hipGetLastError();
 }
 
-hipError_t launch_sample_final(const float* part_val, const int32_t* part_idx, int tiles, int batch,
-                               const int32_t* slot, uint16_t* pen, int vocab, uint32_t* next, uint32_t* ids_cap,
-                               const int32_t* step_ctr, hipStream_t st) {
-    hipLaunchKernelGGL(k_sample_final, dim3(batch), dim3(256), 0, st, part_val, part_idx, tiles, slot, pen, vocab, next,
-                       ids_cap, (int32_t*)step_ctr, batch);
-    return hipGetLastError();
-}
-
-hipError_t launch_step_counter(int32_t* ctr, int reset, hipStream_t st) {
-    hipLaunchKernelGGL(k_step_counter, dim3(1), dim3(1), 0, st, ctr, reset);
+hipError_t launch_sample(const SampleArgs& a, hipStream_t st) {
+    if (a.batch <= 0) return hipSuccess;
+    if (!a.table || a.ssq_tiles != (int)((a.table->k + 63) / 64) || (a.ids_cap && !a.step)) return hipErrorInvalidValue;
+    launch_kernel(k_sample, dim3(a.batch), dim3(256), 0, st, a, *a.table);
     return hipGetLastError();
 }
 

@@ -107,8 +107,8 @@ def silu_mul(plane, g, u):
 
 
 def attn_decode(plane, q, k, v, seq_off, seq_len, n_q, n_kv, head_dim, max_len):
-    """q: [B, n_q*hd] f32; k, v: [n_kv, rows, hd] (f16 or f32); seq_off int64 [B];
-    seq_len int32 [B] (all DeviceArrays)."""
+    """q: [B, n_q*hd] f32; k: [n_kv, rows, hd]; v: [n_kv, rows, hd] in f32 or [n_kv, hd, rows] in
+    f16; seq_off int64 [B]; seq_len int32 [B] (all DeviceArrays)."""
     out = DeviceArray(plane, q.shape, np.float32)
     kv_f16 = 1 if k.dtype == np.float16 else 0
     check(lib.bh_attn_decode(plane.ctx, q.ptr, k.ptr, v.ptr, kv_f16, k.shape[1], seq_off.ptr, seq_len.ptr,

@@ -132,11 +132,13 @@ int bh_rope(bh_ctx* ctx, float* v, const int32_t* pos, int rows, int n_heads, in
 /* out = g * (1 / (1 + exp(-g))) * u   (cpu_engine.rs:2023-2026) */
 int bh_silu_mul(bh_ctx* ctx, const float* g, const float* u, float* out, int64_t n, void* stream);
 /* GQA decode attention for `batch` query rows (flash_attention_single_into,
- * cpu_engine.rs:1450-1509). q: f32 [batch][n_q*head_dim]. k, v: the packed cache,
- * head-major [n_kv][kv_rows][head_dim] in fp16 (kv_f16 = 1) or f32. Row b attends to
- * cache rows [seq_off[b], seq_off[b] + seq_len[b]) (device int64 / int32 arrays; the
- * offsets are prefix sums of the sequences' capacities). max_len bounds seq_len and
- * sizes the split over the context. out: f32 [batch][n_q*head_dim]. */
+ * cpu_engine.rs:1450-1509). q: f32 [batch][n_q*head_dim]. The packed cache: K is head-major
+ * [n_kv][kv_rows][head_dim]; V is [n_kv][kv_rows][head_dim] in f32 (kv_f16 = 0) and transposed,
+ * [n_kv][head_dim][kv_rows], in fp16 (kv_f16 = 1) — the layout the device decoder keeps.
+ * Row b attends to cache rows [seq_off[b], seq_off[b] + seq_len[b]) (device int64 / int32
+ * arrays; the offsets are prefix sums of the sequences' capacities; offsets and kv_rows that
+ * are multiples of 8 take the 16-byte load path). max_len bounds seq_len and sizes the split
+ * over the context. out: f32 [batch][n_q*head_dim]. */
 int bh_attn_decode(bh_ctx* ctx, const float* q, const void* k, const void* v, int kv_f16, int64_t kv_rows,
                    const int64_t* seq_off, const int32_t* seq_len, int batch, int n_q, int n_kv, int head_dim,
                    int max_len, float* out, void* stream);
@@ -194,9 +196,11 @@ int bh_model_generate(bh_model* m, int slot, const uint32_t* prompt, int n_promp
                       int* n_out, float* raw_logits);
 /* Device stream the model's work is ordered on (hipStream_t). */
 void* bh_model_stream(bh_model* m);
-/* Per-kernel timing of the next `n_steps` eager (un-graphed) decode steps: HIP events around
- * every launch of kernel class `kclass` (BH_K_*) on the model's stream. Returns the mean
- * duration in microseconds and the launch count. */
+/* Per-kernel timing of the next `n_steps` eager (un-graphed) decode steps: every kernel of
+ * class `kclass` (BH_K_*) is launched with hipExtLaunchKernelGGL, which records a pair of HIP
+ * events at the kernel's own start and end on the model's stream. Returns the mean duration in
+ * microseconds and the launch count per class. (BH_K_NORM has no launches: the RMSNorm is folded
+ * into the projections.) */
 enum { BH_K_GEMV_QKV = 0, BH_K_ATTN = 1, BH_K_GEMV_O = 2, BH_K_GEMV_GATEUP = 3, BH_K_GEMV_DOWN = 4,
        BH_K_LM_HEAD = 5, BH_K_NORM = 6, BH_K_OTHER = 7, BH_K_COUNT = 8 };
 int bh_model_time_kernels(bh_model* m, int n_steps, double* mean_us /*[BH_K_COUNT]*/,

@@ -183,7 +183,8 @@ def _attn_case(plane, lens, nq=14, nkv=2, hd=64, kv_f16=True, seed=0, check_rows
     k = rng.standard_normal((nkv, rows, hd)).astype(kdt)
     v = rng.standard_normal((nkv, rows, hd)).astype(kdt)
     q = rng.standard_normal((B, nq * hd)).astype(np.float32)
-    out = ops.attn_decode(plane, D(q), D(k), D(v), D(offs), D(np.array(lens, np.int32)), nq, nkv, hd,
+    vdev = np.ascontiguousarray(v.transpose(0, 2, 1)) if kv_f16 else v  # fp16 V is stored [nkv][hd][rows]
+    out = ops.attn_decode(plane, D(q), D(k), D(vdev), D(offs), D(np.array(lens, np.int32)), nq, nkv, hd,
                           int(max(lens))).numpy()
     for b in (check_rows if check_rows is not None else range(B)):
         kc = k[:, offs[b]:offs[b] + lens[b]].astype(np.float32).transpose(1, 0, 2)  # -> [T][nkv][hd]
