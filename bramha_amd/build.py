@@ -15,6 +15,7 @@ LIB = os.path.join(HERE, "libbramha_hip.so")
 OBJ_DIR = os.path.join(ROOT, "_build", "bramha_amd")
 SOURCES = [
     "csrc/k_gemv.hip",
+    "csrc/k_gemm.hip",
     "csrc/k_attn.hip",
     "csrc/k_ops.hip",
     "csrc/bh_host.cpp",

@@ -95,7 +95,8 @@ struct GemvArgs {
     // K split over workgroups: `ksw` workgroups per row tile each store their sums in
     // part[tile * ksw + split][NACC][B][ROWS]; the last to arrive (tile_cnt, reset by it) adds them
     // in split order and runs the epilogue. Needs (tiles * ksw) * NACC * B * ROWS floats of part.
-    int ksw = 1;
+    // ksw = 0 leaves the choice to the launcher (1 without part / tile_cnt).
+    int ksw = 0;
     float* part = nullptr;
     int32_t* tile_cnt = nullptr;
     // EPI_QKV
@@ -130,6 +131,8 @@ inline void launch_kernel(K kernel, dim3 grid, dim3 block, size_t shm, hipStream
 
 // Launchers (k_gemv.hip). Return hipSuccess or the launch error.
 hipError_t launch_gemv(int fmt, int epi, const GemvArgs& a, hipStream_t st);
+// MFMA GEMM pass of B = 16 or 32 tokens over 4-bit weights (k_gemm.hip), rw * 64 rows per tile.
+hipError_t launch_gemm_mf(int fmt, int epi, const GemvArgs& a, int B, int rw, hipStream_t st);
 // Workgroups per row tile for a K-split GEMV over `tiles` row tiles and C chunks.
 int gemv_splits(int tiles, int C, int min_chunks);
 constexpr int MAX_KSW = 16;

@@ -154,17 +154,6 @@ void stream_input(bh_model* m, GemvArgs& a) {
     a.eps = m->c.rms_eps;
 }
 
-// K split over workgroups with the in-kernel ordered reduction, for projections whose few row
-// tiles would leave most CUs idle (each workgroup streams at least min_chunks 16-byte chunks per
-// row; at most max_ksw splits: each split level costs about a microsecond of reduction).
-void split_k(bh_model* m, GemvArgs& a, int min_chunks, int max_ksw) {
-    const int tiles = a.n_pad / 64;
-    a.ksw = std::min(gemv_splits(tiles, a.C, min_chunks), max_ksw);
-    while (a.ksw > 1 && tiles * a.ksw > SPLIT_WG_MAX) --a.ksw;
-    a.part = m->split_part;
-    a.tile_cnt = m->split_cnt;
-}
-
 // Producer side: residual add into x, xw with the next norm's weight, ssq.
 void stream_output(bh_model* m, GemvArgs& a, const float* wnext) {
     a.y = m->x;
@@ -175,12 +164,16 @@ void stream_output(bh_model* m, GemvArgs& a, const float* wnext) {
     a.ssq_tiles = m->ssq_tiles;
 }
 
-void weight_args(GemvArgs& a, const DevWeight& w) {
+// Weight operands; the launcher chooses the K split (ksw 0) and may use the model's split scratch.
+void weight_args(bh_model* m, GemvArgs& a, const DevWeight& w) {
     a.W = w.q;
     a.S = w.s;
     a.N = (int)w.n;
     a.n_pad = (int)w.n_pad;
     a.C = (int)w.chunks;
+    a.ksw = 0;
+    a.part = m->split_part;
+    a.tile_cnt = m->split_cnt;
 }
 
 // One forward pass over M tokens whose residual stream (x, xw, ssq) holds their embedding rows:
@@ -197,7 +190,7 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
     for (int l = 0; l < c.n_layers && e == hipSuccess; ++l) {
         LayerW& w = m->L[l];
         GemvArgs a;
-        weight_args(a, w.qkv);
+        weight_args(m, a, w.qkv);
         stream_input(m, a);
         a.y = m->q;
         a.ldy = m->QD;
@@ -230,7 +223,7 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
         e = timed(m, BH_K_ATTN, [&] { return launch_attention(at, st); });
         if (e != hipSuccess) break;
         GemvArgs o;
-        weight_args(o, w.o);
+        weight_args(m, o, w.o);
         o.x = m->att;
         o.ldx = m->QD;
         o.bias = c.o_bias ? w.bo : nullptr;
@@ -239,7 +232,7 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
         e = timed(m, BH_K_GEMV_O, [&] { return launch_gemv(c.wfmt, EPI_RESNORM, o, st); });
         if (e != hipSuccess) break;
         GemvArgs gu;
-        weight_args(gu, w.gate);
+        weight_args(m, gu, w.gate);
         gu.W2 = w.up.q;
         gu.S2 = w.up.s;
         stream_input(m, gu);
@@ -249,17 +242,16 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
         e = timed(m, BH_K_GEMV_GATEUP, [&] { return launch_gemv(c.wfmt, EPI_SILU, gu, st); });
         if (e != hipSuccess) break;
         GemvArgs d;
-        weight_args(d, w.down);
+        weight_args(m, d, w.down);
         d.x = m->mm;
         d.ldx = I;
         d.batch = M;
         stream_output(m, d, l + 1 < c.n_layers ? m->L[l + 1].ln1 : m->norm);  // final norm after the last layer
-        split_k(m, d, 8, 8);
         e = timed(m, BH_K_GEMV_DOWN, [&] { return launch_gemv(c.wfmt, EPI_RESNORM, d, st); });
     }
     if (e != hipSuccess || !decode) return e;
     GemvArgs lm;
-    weight_args(lm, m->embed);
+    weight_args(m, lm, m->embed);
     stream_input(m, lm);
     lm.y = m->logits;
     lm.ldy = c.vocab;

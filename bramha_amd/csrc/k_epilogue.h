@@ -47,6 +47,48 @@ __device__ __forceinline__ float stream_rnorm(const GemvArgs& a, int b) {
     return 1.0f / sqrtf(t / a.norm_n + a.eps);
 }
 
+// Per-token RMSNorm factors of a normalized residual-stream input (1 without one), into LDS.
+template <int B>
+__device__ __forceinline__ void load_rnorm(const GemvArgs& a, float* rn) {
+    if (threadIdx.x < B) rn[threadIdx.x] = (a.ssq_in && (int)threadIdx.x < a.batch) ? stream_rnorm(a, threadIdx.x) : 1.0f;
+}
+
+// K split over workgroups (a.ksw > 1): publish this split's TOT sums and let the tile's last
+// workgroup add all splits in split order; returns false in every other workgroup, which then
+// exits. The sums are published with agent-scope atomic exchanges and read back with agent-scope
+// atomic loads, both performed at the device-coherent level; the exchanges have returned (the
+// barrier's wait) before the arrival is counted, so the last arrival reads every split's sums
+// without a cache-wide writeback or invalidate. The counter is reset for the next launch.
+template <int TOT>
+__device__ __forceinline__ bool split_reduce(const GemvArgs& a, float* comb, int tile, int kws) {
+    __shared__ int s_last;
+    const int ksw = a.ksw;
+    float* mine = a.part + (int64_t)(tile * ksw + kws) * TOT;
+    float sink = 0.f;
+    for (int i = threadIdx.x; i < TOT; i += blockDim.x)
+        sink += __hip_atomic_exchange(&mine[i], comb[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("" ::"v"(sink));  // the returned values are consumed: the exchanges have completed
+    __syncthreads();
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(&a.tile_cnt[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ksw - 1;
+    __syncthreads();
+    if (!s_last) return false;
+    const float* all = a.part + (int64_t)tile * ksw * TOT;
+    for (int i = threadIdx.x; i < TOT; i += blockDim.x) {
+        // all splits' loads in flight at once (index clamped in bounds), added in split order
+        float v[MAX_KSW];
+#pragma unroll
+        for (int k = 0; k < MAX_KSW; ++k)
+            v[k] = __hip_atomic_load(&all[(int64_t)min(k, ksw - 1) * TOT + i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        float sum = 0.f;
+#pragma unroll
+        for (int k = 0; k < MAX_KSW; ++k) sum += k < ksw ? v[k] : 0.f;
+        comb[i] = sum;
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(&a.tile_cnt[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+}
+
 template <int FMT, int B, int EPI, int ROWS>
 __device__ __forceinline__ void run_epilogue(const GemvArgs& a, const float* fin, float* scratch, const float* rn,
                                              int64_t row0) {

@@ -1,0 +1,218 @@
+// k_gemm.hip — MFMA GEMM for passes of 16 or 32 tokens over 4-bit weights (batched decode
+// and prefill) on gfx950.
+//
+// Reference semantics: gemm_cpu / fused_qkv_gemm (src/inference/cpu_engine.rs:565-912,
+// 3325-3339) and, per token, matvec_mul_into (:1307-1444): Y[b][n] = sum_k W[n][k] X[b][k].
+//
+// Design: a workgroup owns a tile of 64 * RW weight rows and a K range; K splits further over
+// the workgroup's 4 wavefronts per 64-row group (combined in LDS in a fixed order) and, for
+// matrices with few row tiles, over workgroups (the ordered split reduction of k_epilogue.h).
+// Each wavefront runs v_mfma_f32_16x16x32_f16 over its 64 rows as four 16-row A blocks — one
+// dword of 8 nibbles per lane per block, decoded to exact fp16 (q - 8) — with the tokens as the
+// B operand: f32 activations split into fp16 hi + lo (hi + lo carries ~22 bits), so each product
+// takes two MFMAs and the B operand of a chunk is shared by the four row blocks. All loads are
+// raw buffer loads (SGPR resource, per-lane VGPR offset, per-chunk SGPR offset) issued
+// unconditionally (clamped in range) a stage ahead of their use; group-32 fp16 scales multiply
+// each chunk's MFMA result per row; per-row scales are applied in the epilogue.
+#include "bh_internal.h"
+
+#include <hip/hip_fp16.h>
+
+#include "k_epilogue.h"
+#include "k_mfma.h"
+
+namespace bh {
+namespace {
+
+template <int NACC, int TB, int S>
+struct MfStage {
+    uint32_t w[S][NACC][4];  // [chunk][matrix][row block]: dword lg of row rb * 16 + lr
+    uint2 s[S][NACC][4];     // fp16 group scales of rows rb * 16 + 4 lg .. + 3
+    uint4 x[S][TB][2];       // f32 activations of token tb * 16 + lr, k = 8 lg .. + 7
+};
+
+template <int FMT, int B, int EPI, int RW>
+__global__ void __launch_bounds__(256 * RW) k_gemm_mf(const GemvArgs a) {
+    constexpr int NACC = EPI == EPI_SILU ? 2 : 1;
+    constexpr int ROWS = 64 * RW;
+    constexpr int TB = B / 16;
+    constexpr int TOT = NACC * B * ROWS;
+    constexpr int S = 1;  // chunks per pipeline stage (two stages in flight; more costs occupancy)
+    extern __shared__ float smem[];
+    float* rn = smem;          // [32] per-token norm factors
+    float* comb = smem + 32;   // [NACC][B][ROWS] sums, then epilogue scratch [B][ROWS]
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lr = lane & 15, lg = lane >> 4;
+    const int rw = wave % RW, kw = wave / RW;  // 64-row group, K-split index (0..3)
+    const int ksw = a.ksw;
+    const int tiles = gridDim.x / ksw;
+    const int tile = blockIdx.x % tiles, kws = blockIdx.x / tiles;
+    const int per_wg = (a.C + ksw - 1) / ksw;
+    const int wc0 = kws * per_wg, wc1 = min(a.C, wc0 + per_wg);
+    const int per = (max(wc1 - wc0, 0) + 3) / 4;
+    const int c0 = wc0 + kw * per, c1 = min(wc1, c0 + per);
+
+    // the group's 64 rows; a group past the padded matrix re-reads the last one (never stored)
+    const int n0 = min(tile * ROWS + rw * 64, a.n_pad - 64);
+    __amdgpu_buffer_rsrc_t rW[NACC], rS[NACC];
+    rW[0] = __builtin_amdgcn_make_buffer_rsrc((void*)a.W, (short)0, a.C * a.n_pad * 16, 0x00020000);
+    if constexpr (NACC == 2) rW[1] = __builtin_amdgcn_make_buffer_rsrc((void*)a.W2, (short)0, a.C * a.n_pad * 16, 0x00020000);
+    if constexpr (FMT == BH_Q4_G32) {
+        rS[0] = __builtin_amdgcn_make_buffer_rsrc((void*)a.S, (short)0, a.C * a.n_pad * 2, 0x00020000);
+        if constexpr (NACC == 2)
+            rS[1] = __builtin_amdgcn_make_buffer_rsrc((void*)a.S2, (short)0, a.C * a.n_pad * 2, 0x00020000);
+    }
+    const __amdgpu_buffer_rsrc_t rX =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)(a.batch * a.ldx * 4), 0x00020000);
+    const int vo_x = ((int)((lr) * a.ldx) + 8 * lg) * 4;  // token lr (+ tb * 16 rows), k 8 lg
+
+    auto fetch = [&](int c, MfStage<NACC, TB, S>& st) {
+#pragma unroll
+        for (int u = 0; u < S; ++u) {
+            const int cc = min(c + u, c1 - 1);
+#pragma unroll
+            for (int j = 0; j < NACC; ++j)
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) {
+                    st.w[u][j][rb] = __builtin_amdgcn_raw_buffer_load_b32(rW[j], (n0 + rb * 16 + lr) * 16 + 4 * lg,
+                                                                           cc * a.n_pad * 16, 0);
+                    if constexpr (FMT == BH_Q4_G32)
+                        st.s[u][j][rb] = __builtin_bit_cast(
+                            uint2, __builtin_amdgcn_raw_buffer_load_b64(rS[j], (n0 + rb * 16 + 4 * lg) * 2, cc * a.n_pad * 2, 0));
+                }
+#pragma unroll
+            for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    st.x[u][tb][h] = __builtin_bit_cast(
+                        uint4, __builtin_amdgcn_raw_buffer_load_b128(rX, vo_x + (int)(tb * 16 * a.ldx * 4) + h * 16, cc * 128, 0));
+        }
+    };
+
+    f32x4 acc[NACC][4][TB];
+#pragma unroll
+    for (int j = 0; j < NACC; ++j)
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int tb = 0; tb < TB; ++tb) acc[j][rb][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    auto consume = [&](int c, const MfStage<NACC, TB, S>& st) {
+#pragma unroll
+        for (int u = 0; u < S; ++u) {
+            if (c + u < c1) {
+                half8 bh[TB], bl[TB];
+#pragma unroll
+                for (int tb = 0; tb < TB; ++tb)
+                    split8(__builtin_bit_cast(float4, st.x[u][tb][0]), __builtin_bit_cast(float4, st.x[u][tb][1]), bh[tb],
+                           bl[tb]);
+#pragma unroll
+                for (int j = 0; j < NACC; ++j)
+#pragma unroll
+                    for (int rb = 0; rb < 4; ++rb) {
+                        const half8 av = dec8(st.w[u][j][rb]);
+                        if constexpr (FMT == BH_Q4_G32) {
+                            const __half2* s2 = (const __half2*)&st.s[u][j][rb];
+                            const float2 sa = __half22float2(s2[0]), sb = __half22float2(s2[1]);
+#pragma unroll
+                            for (int tb = 0; tb < TB; ++tb) {
+                                f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bh[tb], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                                t = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bl[tb], t, 0, 0, 0);
+                                acc[j][rb][tb][0] = fmaf(sa.x, t[0], acc[j][rb][tb][0]);
+                                acc[j][rb][tb][1] = fmaf(sa.y, t[1], acc[j][rb][tb][1]);
+                                acc[j][rb][tb][2] = fmaf(sb.x, t[2], acc[j][rb][tb][2]);
+                                acc[j][rb][tb][3] = fmaf(sb.y, t[3], acc[j][rb][tb][3]);
+                            }
+                        } else {
+#pragma unroll
+                            for (int tb = 0; tb < TB; ++tb) {
+                                acc[j][rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bh[tb], acc[j][rb][tb], 0, 0, 0);
+                                acc[j][rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bl[tb], acc[j][rb][tb], 0, 0, 0);
+                            }
+                        }
+                    }
+            }
+        }
+    };
+
+    MfStage<NACC, TB, S> s0, s1;
+    if (c0 < c1) fetch(c0, s0);
+    load_rnorm<B>(a, rn);
+    if (c0 < c1) {
+        for (int c = c0;; c += 2 * S) {
+            fetch(c + S, s1);
+            consume(c, s0);
+            if (c + S >= c1) break;
+            fetch(c + 2 * S, s0);
+            consume(c + S, s1);
+            if (c + 2 * S >= c1) break;
+        }
+    }
+
+    // D layout: lane holds token tb * 16 + lr, rows 4 * lg + v of each 16-row block. The four
+    // K-split waves of a row group add into one buffer in turn (a fixed order).
+    constexpr float FIN = FMT == BH_Q4_ROW ? 16.0f : 1.0f;  // row formats: the epilogue scales by s/16
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        if (kw == w) {
+#pragma unroll
+            for (int j = 0; j < NACC; ++j)
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                    for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) {
+                            float* d = &comb[(j * B + tb * 16 + lr) * ROWS + rw * 64 + rb * 16 + 4 * lg + v];
+                            *d = (w == 0 ? 0.f : *d) + acc[j][rb][tb][v] * FIN;
+                        }
+        }
+        __syncthreads();
+    }
+    if (ksw > 1 && !split_reduce<TOT>(a, comb, tile, kws)) return;
+    __syncthreads();
+    run_epilogue<FMT, B, EPI, ROWS>(a, comb, comb + TOT, rn, (int64_t)tile * ROWS);
+}
+
+template <int FMT, int B, int EPI, int RW>
+hipError_t launch_t(const GemvArgs& a, hipStream_t st) {
+    constexpr int NACC = EPI == EPI_SILU ? 2 : 1;
+    constexpr int ROWS = 64 * RW;
+    const int tiles = (a.n_pad + ROWS - 1) / ROWS;
+    const size_t shm = (32 + (size_t)NACC * B * ROWS + (size_t)B * ROWS) * sizeof(float);
+    if (shm > 64 * 1024) return hipErrorInvalidValue;
+    launch_kernel((k_gemm_mf<FMT, B, EPI, RW>), dim3(tiles * a.ksw), dim3(256 * RW), shm, st, a);
+    return hipGetLastError();
+}
+
+template <int FMT, int EPI, int RW>
+hipError_t launch_b(const GemvArgs& a, int B, hipStream_t st) {
+    return B == 32 ? launch_t<FMT, 32, EPI, RW>(a, st) : launch_t<FMT, 16, EPI, RW>(a, st);
+}
+
+template <int FMT>
+hipError_t launch_e(int epi, const GemvArgs& a, int B, int rw, hipStream_t st) {
+    switch (epi) {
+        case EPI_STORE: return launch_b<FMT, EPI_STORE, 1>(a, B, st);
+        case EPI_RESNORM: return launch_b<FMT, EPI_RESNORM, 1>(a, B, st);
+        case EPI_SILU: return launch_b<FMT, EPI_SILU, 1>(a, B, st);
+        case EPI_QKV: return rw == 2 ? launch_b<FMT, EPI_QKV, 2>(a, B, st) : launch_b<FMT, EPI_QKV, 1>(a, B, st);
+        case EPI_LMHEAD:
+            if constexpr (FMT == BH_Q4_G32) return launch_b<FMT, EPI_LMHEAD, 1>(a, B, st);
+            return hipErrorInvalidValue;
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_gemm_mf(int fmt, int epi, const GemvArgs& a, int B, int rw, hipStream_t st) {
+    if ((B != 16 && B != 32) || a.batch != B || a.ksw < 1 || a.n_pad % 64 || rw < 1 || rw > 2) return hipErrorInvalidValue;
+    if (fmt == BH_Q4_G32) return launch_e<BH_Q4_G32>(epi, a, B, rw, st);
+    if (fmt == BH_Q4_ROW) return launch_e<BH_Q4_ROW>(epi, a, B, rw, st);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace bh

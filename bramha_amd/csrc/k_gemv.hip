@@ -82,120 +82,8 @@ __device__ __forceinline__ void decode(const uint4 q, float* v) {
     }
 }
 
-// ---- MFMA path (16 or 32 tokens per pass, 4-bit weights) ----
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-// One dword of a Q4 chunk (8 weights) -> 8 exact fp16 values q - 8 for the A operand of
-// v_mfma_f32_16x16x32_f16. Register pair j holds (nibble j, nibble j + 4): 1024 + q is
-// formed in the fp16 mantissa and 1032 subtracted. Nibble t is element t ^ 1 of the 8
-// (the high nibble of a byte is the even element), so K slot s of the lane holds element
-// kperm(s) = {1, 5, 0, 4, 3, 7, 2, 6}[s]; the activations use the same permutation (the MFMA
-// sum over K is order-free). A function, not a table, so that every index folds at compile time.
-__host__ __device__ constexpr int kperm(int s) { return ((s >> 1) ^ 1) + 4 * (s & 1); }
-
-__device__ __forceinline__ half8 dec8(uint32_t w) {
-    const half2v off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
-    half8 r;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t p = ((w >> (4 * j)) & 0x000F000Fu) | 0x64006400u;
-        const half2v h = __builtin_bit_cast(half2v, p) + off;
-        r[2 * j] = h.x;
-        r[2 * j + 1] = h.y;
-    }
-    return r;
-}
-
-// f32 activations -> fp16 hi + lo (hi + lo carries ~22 bits of the f32 mantissa).
-__device__ __forceinline__ void split8(const float4& x0, const float4& x1, half8& hi, half8& lo) {
-    const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-        const float f = xv[kperm(s)];
-        const _Float16 h = (_Float16)f;
-        hi[s] = h;
-        lo[s] = (_Float16)(f - (float)h);
-    }
-}
-
-// One pipeline stage of the MFMA loop: a chunk's weight dwords, group scales and activations.
-template <int NACC, int TB>
-struct MfStage {
-    uint32_t aw[NACC][4];
-    uint2 sw[NACC][4];
-    float4 xv[TB][2];
-};
-
-template <int FMT, int NACC, int TB>
-__device__ __forceinline__ void mf_fetch(const GemvArgs& a, const uint32_t* const (&Wd)[NACC],
-                                         const __half* const (&Sh)[NACC], int c, int64_t n0, int lr, int lg,
-                                         MfStage<NACC, TB>& st) {
-#pragma unroll
-    for (int j = 0; j < NACC; ++j)
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
-            st.aw[j][rb] = Wd[j][((int64_t)c * a.n_pad + n0 + rb * 16 + lr) * 4 + lg];
-            if constexpr (FMT == BH_Q4_G32)
-                st.sw[j][rb] = *(const uint2*)(Sh[j] + (int64_t)c * a.n_pad + n0 + rb * 16 + 4 * lg);
-        }
-#pragma unroll
-    for (int tb = 0; tb < TB; ++tb) {
-        // rows past the batch read the last row (in bounds) and are zeroed by value selects,
-        // which keeps the stage in registers (a pointer select would move it to scratch)
-        const int m = tb * 16 + lr;
-        const bool ok = m < a.batch;
-        const float4* xp = (const float4*)(a.x + (int64_t)(ok ? m : a.batch - 1) * a.ldx + c * 32 + 8 * lg);
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const float4 v = xp[h];
-            st.xv[tb][h] = make_float4(ok ? v.x : 0.f, ok ? v.y : 0.f, ok ? v.z : 0.f, ok ? v.w : 0.f);
-        }
-    }
-}
-
-template <int FMT, int NACC, int TB>
-__device__ __forceinline__ void mf_consume(const MfStage<NACC, TB>& st, f32x4 (&acc)[NACC][4][TB]) {
-    half8 bh[TB], bl[TB];
-#pragma unroll
-    for (int tb = 0; tb < TB; ++tb) split8(st.xv[tb][0], st.xv[tb][1], bh[tb], bl[tb]);
-#pragma unroll
-    for (int j = 0; j < NACC; ++j) {
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
-            const half8 av = dec8(st.aw[j][rb]);
-            if constexpr (FMT == BH_Q4_G32) {
-                const __half2* s2 = (const __half2*)&st.sw[j][rb];
-                const float2 sa = __half22float2(s2[0]), sb = __half22float2(s2[1]);
-#pragma unroll
-                for (int tb = 0; tb < TB; ++tb) {
-                    f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bh[tb], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bl[tb], t, 0, 0, 0);
-                    acc[j][rb][tb][0] = fmaf(sa.x, t[0], acc[j][rb][tb][0]);
-                    acc[j][rb][tb][1] = fmaf(sa.y, t[1], acc[j][rb][tb][1]);
-                    acc[j][rb][tb][2] = fmaf(sb.x, t[2], acc[j][rb][tb][2]);
-                    acc[j][rb][tb][3] = fmaf(sb.y, t[3], acc[j][rb][tb][3]);
-                }
-            } else {
-#pragma unroll
-                for (int tb = 0; tb < TB; ++tb) {
-                    acc[j][rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bh[tb], acc[j][rb][tb], 0, 0, 0);
-                    acc[j][rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bl[tb], acc[j][rb][tb], 0, 0, 0);
-                }
-            }
-        }
-    }
-}
-
-// Per-token RMSNorm factors of a normalized residual-stream input (1 without one), into LDS.
-template <int B>
-__device__ __forceinline__ void load_rnorm(const GemvArgs& a, float* rn) {
-    if (threadIdx.x < B) rn[threadIdx.x] = (a.ssq_in && (int)threadIdx.x < a.batch) ? stream_rnorm(a, threadIdx.x) : 1.0f;
-}
-
 template <int FMT, int B, int EPI, int RW, int U>
-__global__ void __launch_bounds__(B >= 16 ? 256 : 1024) k_gemv(const GemvArgs a) {
+__global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
     extern __shared__ float smem[];
     float* rn = smem;          // [32] per-token norm factors
     float* comb = smem + 32;   // K-split combine area, then epilogue scratch
@@ -226,61 +114,8 @@ __global__ void __launch_bounds__(B >= 16 ? 256 : 1024) k_gemv(const GemvArgs a)
     // Loads use a clamped row so they are unconditional and in bounds; rows past n_pad (RW = 2
     // tiles) compute values the epilogue never stores.
     const int64_t nl = row_ok ? n : (int64_t)a.n_pad - 1;
-    const uint4* Wp[NACC];
-    const uint16_t* Sp[NACC];
-    Wp[0] = (const uint4*)a.W + nl;
-    Sp[0] = (const uint16_t*)a.S + nl;
-    if constexpr (NACC == 2) {
-        Wp[1] = (const uint4*)a.W2 + nl;
-        Sp[1] = (const uint16_t*)a.S2 + nl;
-    }
 
-    if constexpr (B >= 16) {
-        static_assert(FMT == BH_Q4_G32 || FMT == BH_Q4_ROW, "MFMA path is for 4-bit weights");
-        constexpr int TB = B / 16;
-        const int lr = lane & 15, lg = lane >> 4;
-        const int64_t n0 = (int64_t)tile * ROWS + rw * 64;
-        f32x4 acc[NACC][4][TB];
-#pragma unroll
-        for (int j = 0; j < NACC; ++j)
-#pragma unroll
-            for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-                for (int tb = 0; tb < TB; ++tb) acc[j][rb][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        const uint32_t* Wd[NACC];
-        Wd[0] = (const uint32_t*)a.W;
-        if constexpr (NACC == 2) Wd[1] = (const uint32_t*)a.W2;
-        const __half* Sh[NACC];
-        Sh[0] = (const __half*)a.S;
-        if constexpr (NACC == 2) Sh[1] = (const __half*)a.S2;
-        const bool work = n0 < a.n_pad && c0 < c1;
-        // two stages in flight; the refetch past the end re-reads the last chunk (in bounds, unused)
-        MfStage<NACC, TB> s0, s1;
-        if (work) mf_fetch<FMT>(a, Wd, Sh, c0, n0, lr, lg, s0);
-        load_rnorm<B>(a, rn);
-        if (work) {
-            int c = c0;
-            for (; c + 1 < c1; c += 2) {
-                mf_fetch<FMT>(a, Wd, Sh, c + 1, n0, lr, lg, s1);
-                mf_consume<FMT>(s0, acc);
-                mf_fetch<FMT>(a, Wd, Sh, min(c + 2, c1 - 1), n0, lr, lg, s0);
-                mf_consume<FMT>(s1, acc);
-            }
-            if (c < c1) mf_consume<FMT>(s0, acc);
-        }
-        // D layout of 16x16 MFMA: lane holds column lr (token), rows 4*lg + v
-        constexpr float FIN = FMT == BH_Q4_ROW ? 16.0f : 1.0f;  // row formats: the epilogue scales by s/16
-#pragma unroll
-        for (int j = 0; j < NACC; ++j)
-#pragma unroll
-            for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-                for (int tb = 0; tb < TB; ++tb)
-#pragma unroll
-                    for (int v = 0; v < 4; ++v)
-                        comb[kw * TOT + (j * B + tb * 16 + lr) * ROWS + rw * 64 + rb * 16 + 4 * lg + v] =
-                            acc[j][rb][tb][v] * FIN;
-    } else {
+    {
         // Weight and scale loads are raw buffer loads: an SGPR resource per matrix, the lane's row
         // as the VGPR offset and the chunk as the (uniform) SGPR offset, so a stage costs no
         // per-load address arithmetic. Every load of a stage is unconditional (chunk index
@@ -365,39 +200,7 @@ __global__ void __launch_bounds__(B >= 16 ? 256 : 1024) k_gemv(const GemvArgs a)
         for (int w = 1; w < ksplit; ++w) sum += comb[w * TOT + i];
         comb[i] = sum;
     }
-    if (ksw > 1) {
-        // K split over workgroups: publish this split's sums, and let the tile's last workgroup
-        // add all splits in split order and run the epilogue. The sums are published with
-        // agent-scope atomic exchanges and read back with agent-scope atomic loads, which are
-        // performed at the device-coherent level; the exchanges have returned (the barrier's wait)
-        // before the arrival count is taken, so the last arrival reads every split's sums without
-        // a cache-wide writeback or invalidate.
-        __shared__ int s_last;
-        float* mine = a.part + (int64_t)(tile * ksw + kws) * TOT;
-        float sink = 0.f;
-        for (int i = threadIdx.x; i < TOT; i += blockDim.x)
-            sink += __hip_atomic_exchange(&mine[i], comb[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        asm volatile("" ::"v"(sink));  // the returned values are consumed: the exchanges have completed
-        __syncthreads();
-        if (threadIdx.x == 0)
-            s_last = __hip_atomic_fetch_add(&a.tile_cnt[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ksw - 1;
-        __syncthreads();
-        if (!s_last) return;
-        const float* all = a.part + (int64_t)tile * ksw * TOT;
-        for (int i = threadIdx.x; i < TOT; i += blockDim.x) {
-            // all splits' loads in flight at once (index clamped in bounds), added in split order
-            float v[MAX_KSW];
-#pragma unroll
-            for (int k = 0; k < MAX_KSW; ++k)
-                v[k] = __hip_atomic_load(&all[(int64_t)min(k, ksw - 1) * TOT + i], __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT);
-            float sum = 0.f;
-#pragma unroll
-            for (int k = 0; k < MAX_KSW; ++k) sum += k < ksw ? v[k] : 0.f;
-            comb[i] = sum;
-        }
-        if (threadIdx.x == 0) __hip_atomic_store(&a.tile_cnt[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (ksw > 1 && !split_reduce<TOT>(a, comb, tile, kws)) return;
     __syncthreads();
     run_epilogue<FMT, B, EPI, ROWS>(a, comb, comb + TOT, rn, (int64_t)tile * ROWS);
 }
@@ -419,10 +222,6 @@ hipError_t launch_one(const GemvArgs& a, int ksplit, hipStream_t st) {
 template <int FMT, int EPI, int RW>
 hipError_t launch_b(const GemvArgs& a, int B, int ksplit, int cpw, hipStream_t st) {
     constexpr int NACC = EPI == EPI_SILU ? 2 : 1;
-    if constexpr (FMT == BH_Q4_G32 || FMT == BH_Q4_ROW) {
-        if (B == 32) return launch_one<FMT, 32, EPI, RW, 1>(a, ksplit, st);
-        if (B == 16) return launch_one<FMT, 16, EPI, RW, 1>(a, ksplit, st);
-    }
     if (B <= 2) {
         const bool b1 = B == 1;
         if (cpw <= 2) return b1 ? launch_one<FMT, 1, EPI, RW, 2>(a, ksplit, st) : launch_one<FMT, 2, EPI, RW, 2>(a, ksplit, st);
@@ -452,11 +251,11 @@ hipError_t launch_fmt(int epi, const GemvArgs& a, int B, int rw, int ksplit, int
 
 }  // namespace
 
-// Waves per workgroup along K: aim for ~8 waves per CU and >= 2 chunks per wave
-// (MFMA passes: at most 256 threads per workgroup); the combine area stays under 60 KB.
+// Waves per workgroup along K: aim for ~8 waves per CU and >= 2 chunks per wave; the combine
+// area stays under 60 KB.
 static int waves_per_tile(int tiles, int rw, int C, int nacc, int B) {
-    int ks = ((B >= 16 ? 4096 : 2048) + tiles * rw - 1) / (tiles * rw);
-    ks = std::max(1, std::min({ks, (B >= 16 ? 4 : 16) / rw, std::max(1, C / 2)}));
+    int ks = (2048 + tiles * rw - 1) / (tiles * rw);
+    ks = std::max(1, std::min({ks, 16 / rw, std::max(1, C / 2)}));
     while (ks > 1 && (size_t)ks * nacc * B * 64 * rw * 4 > 60 * 1024) --ks;
     return ks;
 }
@@ -468,26 +267,39 @@ int gemv_splits(int tiles, int C, int min_chunks) {
     return std::max(1, std::min({ksw, MAX_KSW, std::max(1, C / std::max(min_chunks, 1))}));
 }
 
-// Splits the batch into passes: MFMA passes of 32 or 16 rows for 4-bit weights, VALU passes
-// of at most 8 rows otherwise.
+// K splits of one pass when the caller left the choice to the launcher (ksw == 0) and provided
+// split scratch: VALU passes split only long-K matrices with few row tiles; MFMA passes split
+// whenever the row tiles leave CUs idle. Bounded by the scratch (SPLIT_WG_MAX workgroups of
+// SPLIT_TOT_MAX floats).
+static int auto_splits(const GemvArgs& a, bool mfma, int rows_per_tile, int tot) {
+    if (a.ksw > 0) return a.ksw;
+    if (!a.part || !a.tile_cnt || tot > SPLIT_TOT_MAX) return 1;
+    const int tiles = (a.n_pad + rows_per_tile - 1) / rows_per_tile;
+    int ksw;
+    // splits pay for their ordered reduction only on long-K matrices with few row tiles (measured:
+    // the 896-wide projections are fastest unsplit at 1 and at 32 tokens)
+    ksw = (tiles <= 32 && a.C >= 64) ? std::min(gemv_splits(tiles, a.C, 8), mfma ? 16 : 8) : 1;
+    while (ksw > 1 && tiles * ksw > SPLIT_WG_MAX) --ksw;
+    return ksw;
+}
+
+// Splits the batch into passes: MFMA passes of 32 or 16 rows for 4-bit weights (k_gemm.hip),
+// VALU passes of at most 8 rows otherwise.
 hipError_t launch_gemv(int fmt, int epi, const GemvArgs& a0, hipStream_t st) {
     const int rw = (epi == EPI_QKV && a0.hd > 64) ? a0.hd / 64 : 1;
     if (rw > 2) return hipErrorInvalidValue;
     if (a0.ssq_in && a0.batch > 0 && (a0.ssq_tiles <= 0 || a0.norm_n <= 0.f)) return hipErrorInvalidValue;
     if (epi == EPI_RESNORM && (!a0.xw_out || !a0.wnext || !a0.ssq_out || a0.ssq_tiles != a0.n_pad / 64))
         return hipErrorInvalidValue;
-    if (a0.ksw < 1 || a0.ksw > MAX_KSW || (a0.ksw > 1 && (!a0.part || !a0.tile_cnt))) return hipErrorInvalidValue;
-    const int ksw = a0.ksw;
+    if (a0.ksw < 0 || a0.ksw > MAX_KSW || (a0.ksw > 1 && (!a0.part || !a0.tile_cnt))) return hipErrorInvalidValue;
     const int nacc = epi == EPI_SILU ? 2 : 1;
-    const int tiles = (a0.n_pad + 64 * rw - 1) / (64 * rw);
     int b0 = 0;
     while (b0 < a0.batch) {
         const int rem = a0.batch - b0;
         const bool mf = (fmt == BH_Q4_G32 || fmt == BH_Q4_ROW) && rem >= 16;
         const int B = mf ? (rem >= 32 ? 32 : 16) : (rem >= 8 ? 8 : (rem >= 4 ? 4 : (rem >= 2 ? 2 : 1)));
-        const int ks = waves_per_tile(tiles * ksw, rw, (a0.C + ksw - 1) / ksw, nacc, B);
         GemvArgs a = a0;
-        a.batch = std::min(B, rem);
+        a.batch = B;
         a.x = a0.x + (int64_t)b0 * a0.ldx;
         a.y = a0.y + (int64_t)b0 * a0.ldy;
         if (a0.xw_out) a.xw_out = a0.xw_out + (int64_t)b0 * a0.ldy;
@@ -499,14 +311,22 @@ hipError_t launch_gemv(int fmt, int epi, const GemvArgs& a0, hipStream_t st) {
         const int tiles64 = (a0.n_pad + 63) / 64;
         if (a0.part_val) a.part_val = a0.part_val + (int64_t)b0 * tiles64;
         if (a0.part_idx) a.part_idx = a0.part_idx + (int64_t)b0 * tiles64;
-        const int cpw = ((a0.C + ksw - 1) / ksw + ks - 1) / ks;  // chunks per wave
         hipError_t e;
-        switch (fmt) {
-            case BH_F32: e = launch_fmt<BH_F32>(epi, a, B, rw, ks, cpw, st); break;
-            case BH_Q8_ROW: e = launch_fmt<BH_Q8_ROW>(epi, a, B, rw, ks, cpw, st); break;
-            case BH_Q4_ROW: e = launch_fmt<BH_Q4_ROW>(epi, a, B, rw, ks, cpw, st); break;
-            case BH_Q4_G32: e = launch_fmt<BH_Q4_G32>(epi, a, B, rw, ks, cpw, st); break;
-            default: return hipErrorInvalidValue;
+        if (mf) {
+            a.ksw = auto_splits(a0, true, 64 * rw, nacc * B * 64 * rw);
+            e = launch_gemm_mf(fmt, epi, a, B, rw, st);
+        } else {
+            a.ksw = auto_splits(a0, false, 64 * rw, nacc * B * 64 * rw);
+            const int tiles = (a0.n_pad + 64 * rw - 1) / (64 * rw);
+            const int ks = waves_per_tile(tiles * a.ksw, rw, (a0.C + a.ksw - 1) / a.ksw, nacc, B);
+            const int cpw = ((a0.C + a.ksw - 1) / a.ksw + ks - 1) / ks;  // chunks per wave
+            switch (fmt) {
+                case BH_F32: e = launch_fmt<BH_F32>(epi, a, B, rw, ks, cpw, st); break;
+                case BH_Q8_ROW: e = launch_fmt<BH_Q8_ROW>(epi, a, B, rw, ks, cpw, st); break;
+                case BH_Q4_ROW: e = launch_fmt<BH_Q4_ROW>(epi, a, B, rw, ks, cpw, st); break;
+                case BH_Q4_G32: e = launch_fmt<BH_Q4_G32>(epi, a, B, rw, ks, cpw, st); break;
+                default: return hipErrorInvalidValue;
+            }
         }
         if (e != hipSuccess) return e;
         b0 += B;
