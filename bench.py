@@ -77,6 +77,75 @@ def roofline(m, n_steps=16):
                   "launches_per_step": {k: v[1] // n_steps for k, v in t.items()}}
 
 
+# (out_features, in_features) of the Qwen2-0.5B projections: q/o, k/v, gate/up, down, LM head.
+GEMV_SHAPES = ((896, 896), (128, 896), (4864, 896), (896, 4864), (151936, 896))
+GEMV_BATCHES = (1, 4, 16, 32)
+
+
+def gemv_sweep(plane, rotate=1 << 30, iters=64):
+    """Isolated 4-bit GEMV/GEMM: one fp16 scale per 32 weights, weights N(0, 0.02) before
+    quantization, activations N(0, 1). Each launch streams its weight from HBM (graph of
+    launches rotating over >= 1 GiB of weight copies). Bytes = packed nibbles + scales +
+    activations in + outputs."""
+    import numpy as np
+
+    from bramha_amd import BH_Q4_G32, ops
+    from bramha_amd.model import quantize, synth_normal
+
+    out = []
+    for n, k in GEMV_SHAPES:
+        w = synth_normal(0, "sweep.%dx%d" % (n, k), n * k, 0.02).reshape(n, k)
+        q, sc = quantize(BH_Q4_G32, w)
+        del w
+        dw = ops.DeviceWeight(plane, BH_Q4_G32, n, k, q, sc)
+        for b in GEMV_BATCHES:
+            x = ops.DeviceArray.from_numpy(plane, synth_normal(0, "sweep.x", b * k, 1.0).reshape(b, k))
+            y = ops.DeviceArray(plane, (b, n), np.float32)
+            us = dw.time_gemv(x, y, iters=iters, rotate_bytes=rotate)
+            nbytes = n * k * 0.5 + n * k / 32 * 2 + b * k * 4 + b * n * 4
+            r = {"n": n, "k": k, "batch": b, "us": round(us, 3), "GBps": round(nbytes / us / 1e3, 1),
+                 "hbm_frac": round(nbytes / (us * 1e-6) / HBM_PEAK, 4),
+                 "TFLOPs": round(2.0 * n * k * b / us / 1e6, 2)}
+            log("gemv %6dx%-5d B=%-2d %8.2f us %7.1f GB/s (%.1f%% HBM)" %
+                (n, k, b, us, r["GBps"], 100 * r["hbm_frac"]))
+            out.append(r)
+            x.free()
+            y.free()
+        dw.free()
+    return out
+
+
+def attn_sweep(plane, rotate=1 << 30, iters=32, seed=0):
+    """GQA decode attention alone: 14 query heads over 2 KV heads of 64, fp16 K/V N(0, 1) (V
+    stored transposed), one query token per sequence at the end of its context, softmax in f32.
+    Bytes = K + V rows read + queries + outputs."""
+    import numpy as np
+
+    from bramha_amd import ops
+
+    nq, nkv, hd = 14, 2, 64
+    rng = np.random.default_rng(seed)
+    out = []
+    for T in (512, 4096, 32768):
+        for B in (1, 8):
+            rows = T * B
+            k = rng.standard_normal((nkv, rows, hd), dtype=np.float32).astype(np.float16)
+            v = rng.standard_normal((nkv, hd, rows), dtype=np.float32).astype(np.float16)
+            q = rng.standard_normal((B, nq * hd), dtype=np.float32)
+            dk, dv, dq = (ops.DeviceArray.from_numpy(plane, a) for a in (k, v, q))
+            off = ops.DeviceArray.from_numpy(plane, np.arange(B, dtype=np.int64) * T)
+            ln = ops.DeviceArray.from_numpy(plane, np.full(B, T, np.int32))
+            us = ops.time_attn(plane, dq, dk, dv, off, ln, nq, nkv, hd, T, iters=iters, rotate_bytes=rotate)
+            nbytes = 2.0 * rows * nkv * hd * 2 + 2 * B * nq * hd * 4
+            r = {"context": T, "batch": B, "us": round(us, 3), "GBps": round(nbytes / us / 1e3, 1),
+                 "hbm_frac": round(nbytes / (us * 1e-6) / HBM_PEAK, 4)}
+            log("attn T=%-6d B=%d %8.2f us %7.1f GB/s (%.1f%% HBM)" % (T, B, us, r["GBps"], 100 * r["hbm_frac"]))
+            out.append(r)
+            for a in (dk, dv, dq, off, ln):
+                a.free()
+    return out
+
+
 def cpu_baseline(budget_s=15.0, max_steps=64):
     """The reference CPU path (the oracle's restatement of generate_cpu with CPU-only mode):
     Qwen2-0.5B shape, 4-bit per-row projections (the reference's U4 format) and the f32 tied
@@ -113,6 +182,7 @@ def main():
     ap.add_argument("--prompt", type=int, default=32)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-bs1", action="store_true")
+    ap.add_argument("--no-sweeps", action="store_true", help="skip the isolated GEMV and attention sweeps")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -144,6 +214,12 @@ def main():
         log("bs32: %.1f tok/s (%.3f ms/step); dominant kernel %s: %.1f GB/s" %
             (bs32["value"], bs32["ms_per_step"], kern32, roof32["achieved"]))
         m32.close()
+    gsweep = asweep = None
+    if not args.no_sweeps:
+        log("isolated GEMV sweep")
+        gsweep = gemv_sweep(plane)
+        log("isolated attention sweep")
+        asweep = attn_sweep(plane)
     cpu = None
     if not args.no_cpu_baseline:
         log("timing the CPU baseline")
@@ -169,6 +245,8 @@ def main():
         "bs32": bs32,
         "roofline": roof,
         "cpu_baseline": cpu,
+        "gemv_sweep": gsweep,
+        "attn_sweep": asweep,
     }
     print(json.dumps(line), flush=True)
     plane.close()

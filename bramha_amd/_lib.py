@@ -90,6 +90,9 @@ _PROTOS = {
     "bh_rope": (c_int, [_P, _P, _P, c_int, c_int, c_int, c_float, c_int, _P]),
     "bh_silu_mul": (c_int, [_P, _P, _P, _P, c_int64, _P]),
     "bh_attn_decode": (c_int, [_P, _P, _P, _P, c_int, c_int64, _P, _P, c_int, c_int, c_int, c_int, c_int, _P, _P]),
+    "bh_time_gemv": (c_int, [_P, _P, _P, _P, c_int, c_int, c_size_t, POINTER(c_double)]),
+    "bh_time_attn": (c_int, [_P, _P, _P, _P, c_int, c_int64, _P, _P, c_int, c_int, c_int, c_int, c_int, _P, c_int,
+                             c_size_t, POINTER(c_double)]),
     "bh_model_create": (c_int, [_P, POINTER(bh_model_config), POINTER(c_void_p)]),
     "bh_model_destroy": (None, [_P]),
     "bh_model_set_weight": (c_int, [_P, c_char_p, _P, c_size_t, _P, c_size_t]),

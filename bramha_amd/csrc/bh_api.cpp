@@ -15,6 +15,7 @@
 #include <mutex>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 #include "bh_ctx.h"
 
@@ -519,17 +520,10 @@ int bh_silu_mul(bh_ctx* ctx, const float* g, const float* u, float* out, int64_t
     return e == hipSuccess ? BH_OK : ctx->hip_fail(e, "silu launch");
 }
 
-int bh_attn_decode(bh_ctx* ctx, const float* q, const void* k, const void* v, int kv_f16, int64_t kv_rows,
-                   const int64_t* seq_off, const int32_t* seq_len, int batch, int n_q, int n_kv, int head_dim,
-                   int max_len, float* out, void* stream) {
-    if (!ctx || !q || !k || !v || !seq_off || !seq_len || !out || batch < 0 || n_q <= 0 || n_kv <= 0 ||
-        n_q % n_kv || max_len < 0)
-        return BH_ERR_INVALID;
-    if (!attn_supported(n_q, n_kv, head_dim))
-        return ctx->fail(BH_ERR_UNSUPPORTED, "attention supports head_dim 64/128 and 1, 2, 4, 7 or 8 query heads per KV head");
-    if (batch == 0) return BH_OK;
-    std::lock_guard<std::mutex> g(ctx->mu);
-    AttnArgs a;
+// Attention arguments and the split scratch of bh_attn_decode (context lock held).
+static int attn_args(bh_ctx* ctx, const float* q, const void* k, const void* v, int kv_f16, int64_t kv_rows,
+                     const int64_t* seq_off, const int32_t* seq_len, int batch, int n_q, int n_kv, int head_dim,
+                     int max_len, float* out, AttnArgs& a) {
     a.q = q;
     a.out = out;
     a.kv.k = (void*)k;
@@ -566,8 +560,148 @@ int bh_attn_decode(bh_ctx* ctx, const float* q, const void* k, const void* v, in
         }
         a.cnt = ctx->attn_cnt;
     }
+    return BH_OK;
+}
+
+static int attn_check(bh_ctx* ctx, const float* q, const void* k, const void* v, const int64_t* seq_off,
+                      const int32_t* seq_len, float* out, int batch, int n_q, int n_kv, int head_dim, int max_len) {
+    if (!ctx || !q || !k || !v || !seq_off || !seq_len || !out || batch < 0 || n_q <= 0 || n_kv <= 0 ||
+        n_q % n_kv || max_len < 0)
+        return BH_ERR_INVALID;
+    if (!attn_supported(n_q, n_kv, head_dim))
+        return ctx->fail(BH_ERR_UNSUPPORTED, "attention supports head_dim 64/128 and 1, 2, 4, 7 or 8 query heads per KV head");
+    return BH_OK;
+}
+
+int bh_attn_decode(bh_ctx* ctx, const float* q, const void* k, const void* v, int kv_f16, int64_t kv_rows,
+                   const int64_t* seq_off, const int32_t* seq_len, int batch, int n_q, int n_kv, int head_dim,
+                   int max_len, float* out, void* stream) {
+    int rc = attn_check(ctx, q, k, v, seq_off, seq_len, out, batch, n_q, n_kv, head_dim, max_len);
+    if (rc) return rc;
+    if (batch == 0) return BH_OK;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    AttnArgs a;
+    rc = attn_args(ctx, q, k, v, kv_f16, kv_rows, seq_off, seq_len, batch, n_q, n_kv, head_dim, max_len, out, a);
+    if (rc) return rc;
     hipError_t e = launch_attention(a, pick(ctx, stream));
     return e == hipSuccess ? BH_OK : ctx->hip_fail(e, "attention launch");
+}
+
+// ------------------------------------------------------------ measurement
+}  // extern "C"
+
+// Replays a HIP graph of `iters` launches built by `record` (launch i of `copies` rotating
+// operands) and returns the mean time per launch in microseconds.
+template <class F>
+static int time_graph(bh_ctx* ctx, int iters, F&& record, double* us) {
+    hipStream_t st = ctx->stream;
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    hipError_t e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return ctx->hip_fail(e, "hipStreamBeginCapture");
+    hipError_t le = hipSuccess;
+    for (int i = 0; i < iters && le == hipSuccess; ++i) le = record(i, st);
+    e = hipStreamEndCapture(st, &g);
+    if (le != hipSuccess) e = le;
+    if (e == hipSuccess) e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    if (e == hipSuccess) e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    if (e == hipSuccess) e = hipGraphLaunch(ge, st);  // warm-up replay
+    if (e == hipSuccess) e = hipEventRecord(e0, st);
+    const int reps = 3;
+    for (int r = 0; r < reps && e == hipSuccess; ++r) e = hipGraphLaunch(ge, st);
+    if (e == hipSuccess) e = hipEventRecord(e1, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    float ms = 0.f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+    if (e0) hipEventDestroy(e0);
+    if (e1) hipEventDestroy(e1);
+    if (ge) hipGraphExecDestroy(ge);
+    if (g) hipGraphDestroy(g);
+    if (e != hipSuccess) return ctx->hip_fail(e, "timed graph");
+    *us = ms * 1000.0 / ((double)reps * iters);
+    return BH_OK;
+}
+
+extern "C" {
+
+int bh_time_gemv(bh_ctx* ctx, const bh_weight* wh, const float* x, float* y, int batch, int iters,
+                 size_t rotate_bytes, double* us_per_launch) {
+    if (!ctx || !wh || !x || !y || batch <= 0 || iters <= 0 || !us_per_launch) return BH_ERR_INVALID;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    const DevWeight& w = *(const DevWeight*)wh;
+    const int copies = (int)std::max<size_t>(1, std::min<size_t>(4096, (rotate_bytes + w.bytes - 1) / std::max<size_t>(w.bytes, 1)));
+    std::vector<DevWeight> cl(copies);
+    int rc = BH_OK;
+    cl[0] = w;
+    const size_t qb = (size_t)w.chunks * w.n_pad * 16, sb = w.bytes - qb;
+    for (int i = 1; i < copies && rc == BH_OK; ++i) {
+        cl[i] = w;
+        cl[i].q = cl[i].s = nullptr;
+        hipError_t e = hipMalloc(&cl[i].q, qb);
+        if (e == hipSuccess) e = hipMemcpy(cl[i].q, w.q, qb, hipMemcpyDeviceToDevice);
+        if (e == hipSuccess && sb) e = hipMalloc(&cl[i].s, sb);
+        if (e == hipSuccess && sb) e = hipMemcpy(cl[i].s, w.s, sb, hipMemcpyDeviceToDevice);
+        if (e != hipSuccess) rc = ctx->hip_fail(e, "weight copies");
+    }
+    if (rc == BH_OK)
+        rc = time_graph(ctx, iters, [&](int i, hipStream_t st) {
+            const DevWeight& c = cl[i % copies];
+            GemvArgs a;
+            a.W = c.q;
+            a.S = c.s;
+            a.x = x;
+            a.ldx = c.k;
+            a.y = y;
+            a.ldy = c.n;
+            a.N = (int)c.n;
+            a.n_pad = (int)c.n_pad;
+            a.C = (int)c.chunks;
+            a.batch = batch;
+            return launch_gemv(c.fmt, EPI_STORE, a, st);
+        }, us_per_launch);
+    for (int i = 1; i < copies; ++i) {
+        if (cl[i].q) hipFree(cl[i].q);
+        if (cl[i].s) hipFree(cl[i].s);
+    }
+    return rc;
+}
+
+int bh_time_attn(bh_ctx* ctx, const float* q, const void* k, const void* v, int kv_f16, int64_t kv_rows,
+                 const int64_t* seq_off, const int32_t* seq_len, int batch, int n_q, int n_kv, int head_dim,
+                 int max_len, float* out, int iters, size_t rotate_bytes, double* us_per_launch) {
+    int rc = attn_check(ctx, q, k, v, seq_off, seq_len, out, batch, n_q, n_kv, head_dim, max_len);
+    if (rc) return rc;
+    if (batch <= 0 || iters <= 0 || !us_per_launch) return BH_ERR_INVALID;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    AttnArgs a;
+    rc = attn_args(ctx, q, k, v, kv_f16, kv_rows, seq_off, seq_len, batch, n_q, n_kv, head_dim, max_len, out, a);
+    if (rc) return rc;
+    const size_t kvb = (size_t)kv_rows * n_kv * head_dim * (kv_f16 ? 2 : 4);
+    const int copies = (int)std::max<size_t>(1, std::min<size_t>(256, (rotate_bytes + 2 * kvb - 1) / std::max<size_t>(2 * kvb, 1)));
+    std::vector<void*> kc(copies, nullptr), vc(copies, nullptr);
+    kc[0] = (void*)k;
+    vc[0] = (void*)v;
+    for (int i = 1; i < copies && rc == BH_OK; ++i) {
+        hipError_t e = hipMalloc(&kc[i], kvb);
+        if (e == hipSuccess) e = hipMemcpy(kc[i], k, kvb, hipMemcpyDeviceToDevice);
+        if (e == hipSuccess) e = hipMalloc(&vc[i], kvb);
+        if (e == hipSuccess) e = hipMemcpy(vc[i], v, kvb, hipMemcpyDeviceToDevice);
+        if (e != hipSuccess) rc = ctx->hip_fail(e, "KV copies");
+    }
+    if (rc == BH_OK)
+        rc = time_graph(ctx, iters, [&](int i, hipStream_t st) {
+            AttnArgs b = a;
+            b.kv.k = kc[i % copies];
+            b.kv.v = vc[i % copies];
+            return launch_attention(b, st);
+        }, us_per_launch);
+    for (int i = 1; i < copies; ++i) {
+        if (kc[i]) hipFree(kc[i]);
+        if (vc[i]) hipFree(vc[i]);
+    }
+    return rc;
 }
 
 }  // extern "C"

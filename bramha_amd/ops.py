@@ -87,6 +87,15 @@ class DeviceWeight:
         check(lib.bh_dequant(self.plane.ctx, self.handle, out.ptr, None), self.plane.ctx)
         return out
 
+    def time_gemv(self, x, y, iters=64, rotate_bytes=1 << 30):
+        """Mean microseconds of one bh_gemv launch over x -> y (bh_time_gemv): a graph of
+        `iters` launches rotating over device copies of this weight totalling rotate_bytes."""
+        batch = int(np.prod(x.shape)) // self.k
+        us = ctypes.c_double()
+        check(lib.bh_time_gemv(self.plane.ctx, self.handle, x.ptr, y.ptr, batch, iters, rotate_bytes,
+                               ctypes.byref(us)), self.plane.ctx)
+        return us.value
+
 
 def rmsnorm(plane, x, w, eps):
     rows, n = x.shape
@@ -114,6 +123,19 @@ def attn_decode(plane, q, k, v, seq_off, seq_len, n_q, n_kv, head_dim, max_len):
     check(lib.bh_attn_decode(plane.ctx, q.ptr, k.ptr, v.ptr, kv_f16, k.shape[1], seq_off.ptr, seq_len.ptr,
                              q.shape[0], n_q, n_kv, head_dim, max_len, out.ptr, None), plane.ctx)
     return out
+
+
+def time_attn(plane, q, k, v, seq_off, seq_len, n_q, n_kv, head_dim, max_len, iters=64, rotate_bytes=1 << 30):
+    """Mean microseconds of one bh_attn_decode launch (bh_time_attn), K/V rotated over device
+    copies totalling rotate_bytes."""
+    out = DeviceArray(plane, q.shape, np.float32)
+    kv_f16 = 1 if k.dtype == np.float16 else 0
+    us = ctypes.c_double()
+    check(lib.bh_time_attn(plane.ctx, q.ptr, k.ptr, v.ptr, kv_f16, k.shape[1], seq_off.ptr, seq_len.ptr,
+                           q.shape[0], n_q, n_kv, head_dim, max_len, out.ptr, iters, rotate_bytes,
+                           ctypes.byref(us)), plane.ctx)
+    out.free()
+    return us.value
 
 
 def synchronize(plane):

@@ -143,6 +143,18 @@ int bh_attn_decode(bh_ctx* ctx, const float* q, const void* k, const void* v, in
                    const int64_t* seq_off, const int32_t* seq_len, int batch, int n_q, int n_kv, int head_dim,
                    int max_len, float* out, void* stream);
 
+/* ------------------------------------------------------------ measurement */
+/* Measurement helpers (no counterpart in the reference; used by bench.py for the GEMV and
+ * attention sweeps). Each replays a HIP graph of `iters` launches on the context's stream whose
+ * operands rotate over device copies of the weight (or K/V cache) totalling at least
+ * rotate_bytes, so the data streams from HBM rather than the 256 MB Infinity Cache, and returns
+ * the mean time per launch in microseconds. The copies are freed before returning. */
+int bh_time_gemv(bh_ctx* ctx, const bh_weight* w, const float* x, float* y, int batch, int iters,
+                 size_t rotate_bytes, double* us_per_launch);
+int bh_time_attn(bh_ctx* ctx, const float* q, const void* k, const void* v, int kv_f16, int64_t kv_rows,
+                 const int64_t* seq_off, const int32_t* seq_len, int batch, int n_q, int n_kv, int head_dim,
+                 int max_len, float* out, int iters, size_t rotate_bytes, double* us_per_launch);
+
 /* ------------------------------------------------------------ decoder model */
 typedef struct {
     int32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab;
