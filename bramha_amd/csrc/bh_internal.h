@@ -136,6 +136,10 @@ hipError_t launch_gemm_mf(int fmt, int epi, const GemvArgs& a, int B, int rw, hi
 // Workgroups per row tile for a K-split GEMV over `tiles` row tiles and C chunks.
 int gemv_splits(int tiles, int C, int min_chunks);
 constexpr int MAX_KSW = 16;
+// Cache policy of buffer loads for data read once per launch (weights): non-temporal. Used for
+// weights of at least STREAM_BYTES packed bytes.
+constexpr int CPOL_STREAM = 2;
+constexpr size_t STREAM_BYTES = 16u << 20;
 constexpr int SPLIT_WG_MAX = 512;   // tiles * ksw of a split launch
 constexpr int SPLIT_TOT_MAX = 2 * 32 * 128;  // NACC * B * ROWS floats per workgroup
 

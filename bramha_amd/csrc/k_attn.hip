@@ -308,13 +308,37 @@ __device__ __forceinline__ void split_hl(const float* x, half8& hi, half8& lo) {
 // cover rows 32j .. 32j+31 with row group g = i / 4 owning rows 32j + 8g .. 32j + 8g + 7.
 __device__ __forceinline__ int mf_row(int blk, int i) { return 32 * (blk >> 1) + 8 * (i >> 2) + 4 * (blk & 1) + (i & 3); }
 
-template <int HD, int G>
-__global__ void __launch_bounds__(256) k_attn_mf(const AttnArgs a) {
+// K and V^T operands of one 64-row tile for one wave.
+template <int HD>
+struct KvTile {
+    half8 k[4][HD / 32];  // S^T A operand: rows mf_row(blk, lr), head-dim kc*32 + 8lg .. +7
+    half8 v[2][HD / 16];  // O^T A operand: head-dim db*16 + lr, rows 32j + 8lg .. +7
+};
+
+__device__ __forceinline__ unsigned long long ld_agent64(const float* p) {
+    return __hip_atomic_load((const unsigned long long*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 u64_f2(unsigned long long v) {
+    return make_float2(__uint_as_float((unsigned)v), __uint_as_float((unsigned)(v >> 32)));
+}
+
+// One workgroup of NW waves per (query row, KV head, context split). Each wave walks 64-row
+// tiles r0 + 64*(wave + NW*i) of the split with the next tile's K/V loads in flight while the
+// current one is multiplied (two register stages at head_dim 64, one at 128). Scores are kept
+// in the base-2 domain: s2 = (q . k) * log2(e)/sqrt(hd), p = 2^(s2 - m).
+template <int HD, int G, int NW>
+__global__ void __launch_bounds__(64 * NW) k_attn_mf(const AttnArgs a) {
     constexpr int KC = HD / 32;  // 32-wide head-dim chunks of the score product
     constexpr int DB = HD / 16;  // 16-wide head-dim blocks of the value product
+    constexpr int NT = 64 * NW;
+    constexpr int ST = HD == 64 ? 2 : 1;
+    constexpr int HP = HD / 2;   // float2 pairs per head
     __shared__ float q_s[16][HD];
-    __shared__ float w_m[4][16], w_l[4][16];
-    __shared__ float w_o[4][16][HD + 4];
+    __shared__ float w_m[NW][16], w_l[NW][16];
+    __shared__ float w_o[NW][G][HD];
+    __shared__ float f_s[MAX_SPLITS][G];  // split maxima, then their merge weights
+    __shared__ float m_s[MAX_SPLITS][G];  // split sums
+    __shared__ float L_s[G];
     __shared__ int s_last;
 
     const int b = blockIdx.z, h = blockIdx.y, sp = blockIdx.x;
@@ -322,11 +346,11 @@ __global__ void __launch_bounds__(256) k_attn_mf(const AttnArgs a) {
     const int lr = lane & 15, lg = lane >> 4;
 
     // q first: its address depends on nothing loaded
-    constexpr int QPT = 16 * HD / 256;
+    constexpr int QPT = 16 * HD / NT;
     float qreg[QPT];
 #pragma unroll
     for (int k = 0; k < QPT; ++k) {
-        const int i = threadIdx.x + k * 256;
+        const int i = threadIdx.x + k * NT;
         qreg[k] = i / HD < G ? a.q[((int64_t)b * a.nq + h * G) * HD + i] : 0.f;
     }
     const int64_t off = a.boff[b];
@@ -343,15 +367,14 @@ __global__ void __launch_bounds__(256) k_attn_mf(const AttnArgs a) {
     const __half* Vt = (const __half*)a.kv.v + (int64_t)h * HD * a.kv.kv_rows + off;  // + d * kv_rows + t
     const bool v_aligned = ((off | a.kv.kv_rows) & 7) == 0;
 
-    half8 kf[4][KC], vf[2][DB];
-    auto load_tile = [&](int t0) {
+    auto load_tile = [&](KvTile<HD>& T, int t0) {
 #pragma unroll
         for (int blk = 0; blk < 4; ++blk) {
             const int t = t0 + mf_row(blk, lr);
 #pragma unroll
             for (int kc = 0; kc < KC; ++kc) {
-                if (t < r1) kf[blk][kc] = *(const half8*)(Kc + (int64_t)t * HD + kc * 32 + 8 * lg);
-                else kf[blk][kc] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+                if (t < r1) T.k[blk][kc] = *(const half8*)(Kc + (int64_t)t * HD + kc * 32 + 8 * lg);
+                else T.k[blk][kc] = half8{0, 0, 0, 0, 0, 0, 0, 0};
             }
         }
 #pragma unroll
@@ -361,21 +384,24 @@ __global__ void __launch_bounds__(256) k_attn_mf(const AttnArgs a) {
             for (int db = 0; db < DB; ++db) {
                 const __half* p = Vt + (int64_t)(db * 16 + lr) * a.kv.kv_rows + tg;
                 if (v_aligned && tg + 7 < r1) {
-                    vf[j][db] = *(const half8*)p;
+                    T.v[j][db] = *(const half8*)p;
                 } else {
                     half8 v;
 #pragma unroll
                     for (int e = 0; e < 8; ++e) v[e] = tg + e < r1 ? (_Float16)__half2float(p[e]) : (_Float16)0.f;
-                    vf[j][db] = v;
+                    T.v[j][db] = v;
                 }
             }
         }
     };
+
+    const int step = NW * 64;
     const int tfirst = r0 + wave * 64;
-    if (tfirst < r1) load_tile(tfirst);
+    KvTile<HD> A, B;
+    if (tfirst < r1) load_tile(A, tfirst);
 #pragma unroll
     for (int k = 0; k < QPT; ++k) {
-        const int i = threadIdx.x + k * 256;
+        const int i = threadIdx.x + k * NT;
         q_s[i / HD][i % HD] = qreg[k];
     }
     __syncthreads();
@@ -384,14 +410,13 @@ __global__ void __launch_bounds__(256) k_attn_mf(const AttnArgs a) {
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) split_hl(&q_s[lr][kc * 32 + 8 * lg], qh[kc], ql[kc]);
 
-    const float scale = 1.0f / sqrtf((float)HD);
+    const float scale2 = 1.4426950408889634f / sqrtf((float)HD);
     float m = -INFINITY, l = 0.f;  // head lr: running max; this lane's share of the sum
     f32x4 o[DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int t0 = tfirst; t0 < r1; t0 += 4 * 64) {
-        if (t0 != tfirst) load_tile(t0);
+    auto compute = [&](const KvTile<HD>& T, int t0) {
         // S^T: lane holds rows mf_row(blk, 4lg + v) of head lr
         f32x4 sc[4];
 #pragma unroll
@@ -399,8 +424,8 @@ __global__ void __launch_bounds__(256) k_attn_mf(const AttnArgs a) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kc = 0; kc < KC; ++kc) {
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[blk][kc], qh[kc], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[blk][kc], ql[kc], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(T.k[blk][kc], qh[kc], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(T.k[blk][kc], ql[kc], acc, 0, 0, 0);
             }
             sc[blk] = acc;
         }
@@ -410,13 +435,13 @@ __global__ void __launch_bounds__(256) k_attn_mf(const AttnArgs a) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const bool ok = t0 + mf_row(blk, 4 * lg + v) < r1;
-                sc[blk][v] = ok ? sc[blk][v] * scale : -INFINITY;
+                sc[blk][v] = ok ? sc[blk][v] * scale2 : -INFINITY;
                 tmax = fmaxf(tmax, sc[blk][v]);
             }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        const float mn = fmaxf(m, tmax);
-        const float alpha = m == -INFINITY ? 0.f : expf(m - mn);
+        const float mn = fmaxf(m, tmax);  // finite: row t0 of the tile is in range
+        const float alpha = exp2f(m - mn);  // 0 while m is -inf
         m = mn;
         float ps = 0.f;
         float pr[4][4];
@@ -424,7 +449,7 @@ __global__ void __launch_bounds__(256) k_attn_mf(const AttnArgs a) {
         for (int blk = 0; blk < 4; ++blk)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const float p = sc[blk][v] == -INFINITY ? 0.f : expf(sc[blk][v] - mn);
+                const float p = exp2f(sc[blk][v] - mn);  // 0 for masked rows
                 pr[blk][v] = p;
                 ps += p;
             }
@@ -445,11 +470,30 @@ __global__ void __launch_bounds__(256) k_attn_mf(const AttnArgs a) {
             split_hl(pv, ph, pl);
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[j][db], ph, o[db], 0, 0, 0);
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[j][db], pl, o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(T.v[j][db], ph, o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(T.v[j][db], pl, o[db], 0, 0, 0);
             }
         }
+    };
+
+    for (int t = tfirst; t < r1;) {
+        const int t2 = t + step;
+        if constexpr (ST == 2) {
+            if (t2 < r1) load_tile(B, t2);
+            compute(A, t);
+            if (t2 >= r1) break;
+            const int t3 = t2 + step;
+            if (t3 < r1) load_tile(A, t3);
+            compute(B, t2);
+            t = t3;
+        } else {
+            compute(A, t);
+            if (t2 < r1) load_tile(A, t2);
+            t = t2;
+        }
     }
+
+    // combine the waves: log-sum-exp weights, summed in wave order
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
     if (lg == 0) {
@@ -457,48 +501,113 @@ __global__ void __launch_bounds__(256) k_attn_mf(const AttnArgs a) {
         w_l[wave][lr] = l;
     }
     // O^T D layout: lane holds head lr, head-dim db*16 + 4lg + v
+    if (lr < G) {
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+        for (int db = 0; db < DB; ++db)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) w_o[wave][lr][db * 16 + 4 * lg + v] = o[db][v];
+            for (int v = 0; v < 4; ++v) w_o[wave][lr][db * 16 + 4 * lg + v] = o[db][v];
+    }
     __syncthreads();
 
-    const int64_t hq0 = (int64_t)b * a.nq + h * G;
-    for (int i = threadIdx.x; i < G * HD; i += blockDim.x) {
-        const int g = i / HD, d = i % HD;
+    const int64_t hq0 = (int64_t)b * a.nq + h * G;   // first query head of this KV head
+    const int64_t bh = (int64_t)b * a.nkv + h;
+    const int S = a.splits;
+    float sink = 0.f;
+    for (int i = threadIdx.x; i < G * HP; i += NT) {
+        const int g = i / HP, d = 2 * (i % HP);
         float M = -INFINITY;
-        for (int w = 0; w < 4; ++w) M = fmaxf(M, w_m[w][g]);
-        float L = 0.f, O = 0.f;
-        for (int w = 0; w < 4; ++w) {
-            const float f = w_m[w][g] == -INFINITY ? 0.f : expf(w_m[w][g] - M);
+#pragma unroll
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, w_m[w][g]);
+        float L = 0.f, O0 = 0.f, O1 = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const float f = w_m[w][g] == -INFINITY ? 0.f : exp2f(w_m[w][g] - M);
             L += w_l[w][g] * f;
-            O += w_o[w][g][d] * f;
+            O0 += w_o[w][g][d] * f;
+            O1 += w_o[w][g][d + 1] * f;
         }
-        if (a.splits == 1) {
-            a.out[(hq0 + g) * HD + d] = O * (1.0f / L);
+        if (S == 1) {
+            const float r = L > 0.f ? 1.0f / L : 0.f;
+            *(float2*)&a.out[(hq0 + g) * HD + d] = make_float2(O0 * r, O1 * r);
         } else {
-            a.part_o[((hq0 + g) * a.splits + sp) * HD + d] = O;
+            // partials [b][kv head][split][G][HD] and (m, l) [b][kv head][split][G]
+            const unsigned long long ov =
+                (unsigned long long)__float_as_uint(O0) | ((unsigned long long)__float_as_uint(O1) << 32);
+            float* po = a.part_o + ((bh * S + sp) * G + g) * HD + d;
+            sink += __uint_as_float((unsigned)__hip_atomic_exchange((unsigned long long*)po, ov, __ATOMIC_RELAXED,
+                                                                    __HIP_MEMORY_SCOPE_AGENT));
             if (d == 0) {
-                a.part_ml[((hq0 + g) * a.splits + sp) * 2] = M;
-                a.part_ml[((hq0 + g) * a.splits + sp) * 2 + 1] = L;
+                const unsigned long long mv =
+                    (unsigned long long)__float_as_uint(M) | ((unsigned long long)__float_as_uint(L) << 32);
+                float* pm = a.part_ml + ((bh * S + sp) * G + g) * 2;
+                sink += __uint_as_float((unsigned)__hip_atomic_exchange((unsigned long long*)pm, mv, __ATOMIC_RELAXED,
+                                                                        __HIP_MEMORY_SCOPE_AGENT));
             }
         }
     }
-    if (a.splits == 1) return;
-    __threadfence();
+    if (S == 1) return;
+    asm volatile("" ::"v"(sink));  // the returned values are consumed: the exchanges have completed
     __syncthreads();
-    if (threadIdx.x == 0) s_last = atomicAdd(&a.cnt[b * a.nkv + h], 1) == a.splits - 1;
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(&a.cnt[bh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
-    merge_splits<HD, G>(a, hq0);
-    if (threadIdx.x == 0) a.cnt[b * a.nkv + h] = 0;  // ready for the next launch
+
+    // last workgroup of (b, h): every split's (m, l) into LDS in one round of loads, then per
+    // head M = max m_s, weights f_s = 2^(m_s - M), L = sum l_s f_s
+    const float* pml = a.part_ml + bh * S * G * 2;
+    for (int i = threadIdx.x; i < S * G; i += NT) {
+        const float2 ml = u64_f2(ld_agent64(pml + (int64_t)i * 2));
+        f_s[i / G][i % G] = ml.x;
+        m_s[i / G][i % G] = ml.y;
+    }
+    __syncthreads();
+    for (int g = wave; g < G; g += NW) {
+        float mx = -INFINITY;
+        for (int s2 = lane; s2 < S; s2 += 64) mx = fmaxf(mx, f_s[s2][g]);
+        mx = wave_max(mx);
+        float sum = 0.f;
+        for (int s2 = lane; s2 < S; s2 += 64) {
+            const float ms = f_s[s2][g];
+            const float f = ms == -INFINITY ? 0.f : exp2f(ms - mx);
+            f_s[s2][g] = f;
+            sum += m_s[s2][g] * f;
+        }
+        sum = wave_sum(sum);
+        if (lane == 0) L_s[g] = sum;
+    }
+    __syncthreads();
+    const float* po = a.part_o + bh * S * G * HD;
+    constexpr int U = 32;
+    for (int i = threadIdx.x; i < G * HP; i += NT) {
+        const int g = i / HP, d = 2 * (i % HP);
+        float O0 = 0.f, O1 = 0.f;
+        for (int s0 = 0; s0 < S; s0 += U) {
+            unsigned long long v[U];
+#pragma unroll
+            for (int k = 0; k < U; ++k) v[k] = ld_agent64(po + ((int64_t)min(s0 + k, S - 1) * G + g) * HD + d);
+#pragma unroll
+            for (int k = 0; k < U; ++k) {
+                if (s0 + k < S) {
+                    const float2 x = u64_f2(v[k]);
+                    const float f = f_s[s0 + k][g];
+                    O0 += x.x * f;
+                    O1 += x.y * f;
+                }
+            }
+        }
+        const float r = L_s[g] > 0.f ? 1.0f / L_s[g] : 0.f;
+        *(float2*)&a.out[(hq0 + g) * HD + d] = make_float2(O0 * r, O1 * r);
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(&a.cnt[bh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int HD, int KVF16, int G>
 hipError_t launch_t(const AttnArgs& a, hipStream_t st) {
-    if constexpr (KVF16) launch_kernel((k_attn_mf<HD, G>), dim3(a.splits, a.nkv, a.batch), dim3(256), 0, st, a);
-    else launch_kernel((k_attn<HD, 0, G>), dim3(a.splits, a.nkv, a.batch), dim3(256), 0, st, a);
+    if constexpr (KVF16) {
+        if (a.split_rows >= 512) launch_kernel((k_attn_mf<HD, G, 8>), dim3(a.splits, a.nkv, a.batch), dim3(512), 0, st, a);
+        else launch_kernel((k_attn_mf<HD, G, 4>), dim3(a.splits, a.nkv, a.batch), dim3(256), 0, st, a);
+    } else launch_kernel((k_attn<HD, 0, G>), dim3(a.splits, a.nkv, a.batch), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 
@@ -516,20 +625,26 @@ hipError_t launch_g(const AttnArgs& a, hipStream_t st) {
 
 }  // namespace
 
-// Context split: 256 rows per workgroup (one 64-row tile per wave). Contexts up to 512 rows
-// stay in one workgroup per (row, KV head) — its waves loop over at most two tiles, cheaper
-// than the cross-workgroup merge; at most 128 splits (longer splits loop over tiles).
+// Context split. Up to 1024 rows a (row, KV head) stays in one workgroup (each wave takes at
+// most two 64-row tiles, cheaper than a merge). Longer contexts are cut into splits of at
+// least 256 rows, as many as it takes to give the chip about two workgroups per CU, at most
+// 128. Splits of 512 rows or more run 8 waves per workgroup, shorter ones 4.
+constexpr int ATTN_TARGET_WG = 512;
+constexpr int ATTN_MIN_ROWS = 256;
 void attn_plan(int max_len, int batch, int nkv, int* splits, int* split_rows) {
-    (void)batch;
-    (void)nkv;
     max_len = std::max(max_len, 1);
-    int rows = max_len <= 512 ? 512 : 256;
-    int s = (max_len + rows - 1) / rows;
-    if (s > MAX_SPLITS) {
-        rows = ((max_len + MAX_SPLITS - 1) / MAX_SPLITS + 255) / 256 * 256;
-        s = (max_len + rows - 1) / rows;
+    if (max_len <= 1024) {
+        *splits = 1;
+        *split_rows = (max_len + 63) / 64 * 64;
+        return;
     }
-    *splits = s;
+    const int heads = std::max(batch * nkv, 1);
+    const int want = std::max(1, (ATTN_TARGET_WG + heads - 1) / heads);
+    int rows = (max_len + want - 1) / want;
+    rows = std::max(rows, ATTN_MIN_ROWS);
+    rows = std::max(rows, (max_len + MAX_SPLITS - 1) / MAX_SPLITS);
+    rows = (rows + 255) / 256 * 256;
+    *splits = (max_len + rows - 1) / rows;
     *split_rows = rows;
 }
 

@@ -82,7 +82,7 @@ __device__ __forceinline__ void decode(const uint4 q, float* v) {
     }
 }
 
-template <int FMT, int B, int EPI, int RW, int U>
+template <int FMT, int B, int EPI, int RW, int U, int CP>
 __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
     extern __shared__ float smem[];
     float* rn = smem;          // [32] per-token norm factors
@@ -137,8 +137,8 @@ __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
                 const int cc = min(c + u, c1 - 1);
 #pragma unroll
                 for (int j = 0; j < NACC; ++j) {
-                    q[j][u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rW[j], vo_w, cc * a.n_pad * 16, 0));
-                    if constexpr (FMT == BH_Q4_G32) s[j][u] = __builtin_amdgcn_raw_buffer_load_b16(rS[j], vo_s, cc * a.n_pad * 2, 0);
+                    q[j][u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rW[j], vo_w, cc * a.n_pad * 16, CP));
+                    if constexpr (FMT == BH_Q4_G32) s[j][u] = __builtin_amdgcn_raw_buffer_load_b16(rS[j], vo_s, cc * a.n_pad * 2, CP);
                 }
             }
         };
@@ -213,7 +213,13 @@ hipError_t launch_one(const GemvArgs& a, int ksplit, hipStream_t st) {
     size_t shm = (size_t)ksplit * NACC * B * ROWS * sizeof(float);
     if (EPI == EPI_LMHEAD || EPI == EPI_RESNORM) shm = std::max(shm, (size_t)(NACC * B * ROWS + B * ROWS) * sizeof(float));
     shm += 32 * sizeof(float);
-    launch_kernel((k_gemv<FMT, B, EPI, RW, U>), dim3(tiles), dim3(64 * RW * ksplit), shm, st, a);
+    // non-temporal weight loads pay off on weights far larger than the caches (LM head: 20 us
+    // instead of 22) and cost latency-bound small ones ~0.2 us
+    if (FMT == BH_Q4_G32 && (size_t)a.C * a.n_pad * 16 >= STREAM_BYTES)
+        launch_kernel((k_gemv<FMT, B, EPI, RW, U, FMT == BH_Q4_G32 ? CPOL_STREAM : 0>), dim3(tiles), dim3(64 * RW * ksplit),
+                      shm, st, a);
+    else
+        launch_kernel((k_gemv<FMT, B, EPI, RW, U, 0>), dim3(tiles), dim3(64 * RW * ksplit), shm, st, a);
     return hipGetLastError();
 }
 
@@ -251,10 +257,11 @@ hipError_t launch_fmt(int epi, const GemvArgs& a, int B, int rw, int ksplit, int
 
 }  // namespace
 
-// Waves per workgroup along K: aim for ~8 waves per CU and >= 2 chunks per wave; the combine
-// area stays under 60 KB.
+// Waves per workgroup along K: aim for ~32 waves per CU and >= 2 chunks per wave; the combine
+// area stays under 60 KB. (Measured on the 151936 x 896 LM head: 4 waves per row tile stream
+// 3.5 TB/s where 1 wave per tile streams 2.8.)
 static int waves_per_tile(int tiles, int rw, int C, int nacc, int B) {
-    int ks = (2048 + tiles * rw - 1) / (tiles * rw);
+    int ks = (8192 + tiles * rw - 1) / (tiles * rw);
     ks = std::max(1, std::min({ks, 16 / rw, std::max(1, C / 2)}));
     while (ks > 1 && (size_t)ks * nacc * B * 64 * rw * 4 > 60 * 1024) --ks;
     return ks;
