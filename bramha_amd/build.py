@@ -16,6 +16,7 @@ OBJ_DIR = os.path.join(ROOT, "_build", "bramha_amd")
 SOURCES = [
     "csrc/k_gemv.hip",
     "csrc/k_gemm.hip",
+    "csrc/k_prefill.hip",
     "csrc/k_attn.hip",
     "csrc/k_ops.hip",
     "csrc/bh_host.cpp",

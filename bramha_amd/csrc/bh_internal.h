@@ -113,6 +113,24 @@ struct GemvArgs {
     int32_t* part_idx = nullptr;
 };
 
+// The arguments of tokens b0 .. b0 + n - 1 of `a`: every per-token pointer advanced by b0.
+__host__ __device__ inline GemvArgs gemv_tokens(const GemvArgs& a0, int b0, int n) {
+    GemvArgs a = a0;
+    a.batch = n;
+    a.x = a0.x + (int64_t)b0 * a0.ldx;
+    a.y = a0.y + (int64_t)b0 * a0.ldy;
+    if (a0.xw_out) a.xw_out = a0.xw_out + (int64_t)b0 * a0.ldy;
+    if (a0.ssq_in) a.ssq_in = a0.ssq_in + (int64_t)b0 * a0.ssq_tiles;
+    if (a0.ssq_out) a.ssq_out = a0.ssq_out + (int64_t)b0 * a0.ssq_tiles;
+    if (a0.pos) a.pos = a0.pos + b0;
+    if (a0.boff) a.boff = a0.boff + b0;
+    if (a0.slot) a.slot = a0.slot + b0;
+    const int tiles64 = (a0.n_pad + 63) / 64;
+    if (a0.part_val) a.part_val = a0.part_val + (int64_t)b0 * tiles64;
+    if (a0.part_idx) a.part_idx = a0.part_idx + (int64_t)b0 * tiles64;
+    return a;
+}
+
 // Per-launch timing: while `launch_events` is set (bh_model_time_kernels), every kernel is
 // launched with hipExtLaunchKernelGGL, which records the two events at the kernel's own start
 // and end on its stream (no separate event commands around the launch).
@@ -133,6 +151,10 @@ inline void launch_kernel(K kernel, dim3 grid, dim3 block, size_t shm, hipStream
 hipError_t launch_gemv(int fmt, int epi, const GemvArgs& a, hipStream_t st);
 // MFMA GEMM pass of B = 16 or 32 tokens over 4-bit weights (k_gemm.hip), rw * 64 rows per tile.
 hipError_t launch_gemm_mf(int fmt, int epi, const GemvArgs& a, int B, int rw, hipStream_t st);
+// MFMA GEMM over all a.batch tokens at once for prefill chunks (k_prefill.hip): 128-row by
+// 128-token tiles (64 tokens for the gate/up pair). Not for EPI_LMHEAD.
+hipError_t launch_gemm_pf(int fmt, int epi, const GemvArgs& a, hipStream_t st);
+constexpr int PF_MIN_TOKENS = 64;  // launch_gemv hands passes of at least this many tokens to it
 // Workgroups per row tile for a K-split GEMV over `tiles` row tiles and C chunks.
 int gemv_splits(int tiles, int C, int min_chunks);
 constexpr int MAX_KSW = 16;
@@ -186,6 +208,9 @@ struct AttnArgs {
     const int32_t* seq_len = nullptr;  // standalone mode: explicit lengths [batch] (pos unused)
     int batch = 0, nq = 0, nkv = 0, hd = 0;
     int splits = 1, split_rows = 0;    // context split: rows per split (multiple of 64)
+    // prefill: the batch rows are consecutive tokens of one sequence starting at KV row boff[0]
+    // (fp16 cache: one workgroup per 16 tokens and query head; splits unused)
+    int prefill = 0;
     float* part_o = nullptr;           // [batch][nq][splits][hd]
     float* part_ml = nullptr;          // [batch][nq][splits][2]
 };

@@ -220,6 +220,7 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
         at.part_o = m->attn_part;
         at.part_ml = m->attn_part + (size_t)c.max_tokens * c.n_heads * m->max_splits * c.head_dim;
         at.cnt = m->attn_cnt;
+        at.prefill = decode ? 0 : 1;
         e = timed(m, BH_K_ATTN, [&] { return launch_attention(at, st); });
         if (e != hipSuccess) break;
         GemvArgs o;

@@ -322,16 +322,156 @@ __device__ __forceinline__ float2 u64_f2(unsigned long long v) {
     return make_float2(__uint_as_float((unsigned)v), __uint_as_float((unsigned)(v >> 32)));
 }
 
-// One workgroup of NW waves per (query row, KV head, context split). Each wave walks 64-row
-// tiles r0 + 64*(wave + NW*i) of the split with the next tile's K/V loads in flight while the
-// current one is multiplied (two register stages at head_dim 64, one at 128). Scores are kept
-// in the base-2 domain: s2 = (q . k) * log2(e)/sqrt(hd), p = 2^(s2 - m).
+// The wave's share of a context range for the 16 query columns held as fp16 hi + lo (qh, ql):
+// 64-row tiles r0 + 64*(wave + NW*i) below r1, with the next tile's K/V loads in flight while
+// the current one is multiplied (two register stages at head_dim 64, one at 128). Row t is
+// valid for the lane's column while t < lim (the causal limit of the column). Scores are kept in
+// the base-2 domain: s2 = (q . k) * log2(e)/sqrt(hd), p = 2^(s2 - m). On return m is the
+// column's running max, l this lane's share of its sum and o its unnormalised output
+// (O^T layout: head-dim db*16 + 4lg + v). MASKCOL: columns may have no valid row in a tile.
+// start() issues the loads of the wave's first tile (before the caller waits on its queries),
+// run() multiplies.
+template <int HD, int NW, bool MASKCOL>
+struct AttnWave {
+    static constexpr int KC = HD / 32;  // 32-wide head-dim chunks of the score product
+    static constexpr int DB = HD / 16;  // 16-wide head-dim blocks of the value product
+    static constexpr int ST = HD == 64 ? 2 : 1;
+    const __half* Kc;
+    const __half* Vt;
+    int64_t kv_rows;
+    bool v_aligned;
+    int r0, r1, lim;
+    KvTile<HD> A, B;
+
+    __device__ __forceinline__ void load_tile(KvTile<HD>& T, int t0) const {
+        const int lane = threadIdx.x & 63;
+        const int lr = lane & 15, lg = lane >> 4;
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk) {
+            const int t = t0 + mf_row(blk, lr);
+#pragma unroll
+            for (int kc = 0; kc < KC; ++kc) {
+                if (t < r1) T.k[blk][kc] = *(const half8*)(Kc + (int64_t)t * HD + kc * 32 + 8 * lg);
+                else T.k[blk][kc] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int tg = t0 + 32 * j + 8 * lg;  // this lane group's 8 rows
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                const __half* p = Vt + (int64_t)(db * 16 + lr) * kv_rows + tg;
+                if (v_aligned && tg + 7 < r1) {
+                    T.v[j][db] = *(const half8*)p;
+                } else {
+                    half8 v;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[e] = tg + e < r1 ? (_Float16)__half2float(p[e]) : (_Float16)0.f;
+                    T.v[j][db] = v;
+                }
+            }
+        }
+    }
+
+    __device__ __forceinline__ void start() {
+        const int t = r0 + (int)(threadIdx.x >> 6) * 64;
+        if (t < r1) load_tile(A, t);
+    }
+
+    __device__ __forceinline__ void compute(const KvTile<HD>& T, int t0, const half8 (&qh)[KC], const half8 (&ql)[KC],
+                                            float& m, float& l, f32x4 (&o)[DB]) const {
+        const int lane = threadIdx.x & 63;
+        const int lg = lane >> 4;
+        const float scale2 = 1.4426950408889634f / sqrtf((float)HD);
+        // S^T: lane holds rows mf_row(blk, 4lg + v) of column lr
+        f32x4 sc[4];
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kc = 0; kc < KC; ++kc) {
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(T.k[blk][kc], qh[kc], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(T.k[blk][kc], ql[kc], acc, 0, 0, 0);
+            }
+            sc[blk] = acc;
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const bool ok = t0 + mf_row(blk, 4 * lg + v) < lim;
+                sc[blk][v] = ok ? sc[blk][v] * scale2 : -INFINITY;
+                tmax = fmaxf(tmax, sc[blk][v]);
+            }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float mn = fmaxf(m, tmax);  // without MASKCOL finite: row t0 of the tile is valid
+        float alpha = exp2f(m - mn);      // 0 while m is -inf
+        if constexpr (MASKCOL) alpha = mn == -INFINITY ? 1.f : alpha;
+        m = mn;
+        float ps = 0.f;
+        float pr[4][4];
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                float p = exp2f(sc[blk][v] - mn);  // 0 for masked rows
+                if constexpr (MASKCOL) p = sc[blk][v] == -INFINITY ? 0.f : p;
+                pr[blk][v] = p;
+                ps += p;
+            }
+        l = l * alpha + ps;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) o[db] *= alpha;
+        // O^T += V^T . P^T over rows 32j .. 32j+31: the lane's P slots s = 0..3 are block 2j,
+        // s = 4..7 block 2j+1 — rows 32j + 8lg + s, the rows of its V^T operand
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            float pv[8];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                pv[v] = pr[2 * j][v];
+                pv[4 + v] = pr[2 * j + 1][v];
+            }
+            half8 ph, pl;
+            split_hl(pv, ph, pl);
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(T.v[j][db], ph, o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(T.v[j][db], pl, o[db], 0, 0, 0);
+            }
+        }
+    }
+
+    __device__ __forceinline__ void run(const half8 (&qh)[KC], const half8 (&ql)[KC], float& m, float& l, f32x4 (&o)[DB]) {
+        const int step = NW * 64;
+        for (int t = r0 + (int)(threadIdx.x >> 6) * 64; t < r1;) {
+            const int t2 = t + step;
+            if constexpr (ST == 2) {
+                if (t2 < r1) load_tile(B, t2);
+                compute(A, t, qh, ql, m, l, o);
+                if (t2 >= r1) break;
+                const int t3 = t2 + step;
+                if (t3 < r1) load_tile(A, t3);
+                compute(B, t2, qh, ql, m, l, o);
+                t = t3;
+            } else {
+                compute(A, t, qh, ql, m, l, o);
+                if (t2 < r1) load_tile(A, t2);
+                t = t2;
+            }
+        }
+    }
+};
+
+// Decode: one workgroup of NW waves per (query row, KV head, context split); the G query heads
+// of the KV head are the MFMA columns.
 template <int HD, int G, int NW>
 __global__ void __launch_bounds__(64 * NW) k_attn_mf(const AttnArgs a) {
     constexpr int KC = HD / 32;  // 32-wide head-dim chunks of the score product
     constexpr int DB = HD / 16;  // 16-wide head-dim blocks of the value product
     constexpr int NT = 64 * NW;
-    constexpr int ST = HD == 64 ? 2 : 1;
     constexpr int HP = HD / 2;   // float2 pairs per head
     __shared__ float q_s[16][HD];
     __shared__ float w_m[NW][16], w_l[NW][16];
@@ -365,133 +505,26 @@ __global__ void __launch_bounds__(64 * NW) k_attn_mf(const AttnArgs a) {
     const int r1 = min(len, r0 + a.split_rows);
     const __half* Kc = (const __half*)a.kv.k + ((int64_t)h * a.kv.kv_rows + off) * HD;
     const __half* Vt = (const __half*)a.kv.v + (int64_t)h * HD * a.kv.kv_rows + off;  // + d * kv_rows + t
-    const bool v_aligned = ((off | a.kv.kv_rows) & 7) == 0;
+    AttnWave<HD, NW, false> aw{Kc, Vt, a.kv.kv_rows, ((off | a.kv.kv_rows) & 7) == 0, r0, r1, r1};
+    aw.start();
 
-    auto load_tile = [&](KvTile<HD>& T, int t0) {
-#pragma unroll
-        for (int blk = 0; blk < 4; ++blk) {
-            const int t = t0 + mf_row(blk, lr);
-#pragma unroll
-            for (int kc = 0; kc < KC; ++kc) {
-                if (t < r1) T.k[blk][kc] = *(const half8*)(Kc + (int64_t)t * HD + kc * 32 + 8 * lg);
-                else T.k[blk][kc] = half8{0, 0, 0, 0, 0, 0, 0, 0};
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int tg = t0 + 32 * j + 8 * lg;  // this lane group's 8 rows
-#pragma unroll
-            for (int db = 0; db < DB; ++db) {
-                const __half* p = Vt + (int64_t)(db * 16 + lr) * a.kv.kv_rows + tg;
-                if (v_aligned && tg + 7 < r1) {
-                    T.v[j][db] = *(const half8*)p;
-                } else {
-                    half8 v;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) v[e] = tg + e < r1 ? (_Float16)__half2float(p[e]) : (_Float16)0.f;
-                    T.v[j][db] = v;
-                }
-            }
-        }
-    };
-
-    const int step = NW * 64;
-    const int tfirst = r0 + wave * 64;
-    KvTile<HD> A, B;
-    if (tfirst < r1) load_tile(A, tfirst);
+    // q rows into LDS, then Q^T as the B operand:
+    // lane (lr, lg) holds head lr, head-dim kc*32 + 8lg .. +7
 #pragma unroll
     for (int k = 0; k < QPT; ++k) {
         const int i = threadIdx.x + k * NT;
         q_s[i / HD][i % HD] = qreg[k];
     }
     __syncthreads();
-    // Q^T as the B operand: lane (lr, lg) holds head lr, head-dim kc*32 + 8lg .. +7
     half8 qh[KC], ql[KC];
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) split_hl(&q_s[lr][kc * 32 + 8 * lg], qh[kc], ql[kc]);
 
-    const float scale2 = 1.4426950408889634f / sqrtf((float)HD);
-    float m = -INFINITY, l = 0.f;  // head lr: running max; this lane's share of the sum
+    float m = -INFINITY, l = 0.f;
     f32x4 o[DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    auto compute = [&](const KvTile<HD>& T, int t0) {
-        // S^T: lane holds rows mf_row(blk, 4lg + v) of head lr
-        f32x4 sc[4];
-#pragma unroll
-        for (int blk = 0; blk < 4; ++blk) {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int kc = 0; kc < KC; ++kc) {
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(T.k[blk][kc], qh[kc], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(T.k[blk][kc], ql[kc], acc, 0, 0, 0);
-            }
-            sc[blk] = acc;
-        }
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int blk = 0; blk < 4; ++blk)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const bool ok = t0 + mf_row(blk, 4 * lg + v) < r1;
-                sc[blk][v] = ok ? sc[blk][v] * scale2 : -INFINITY;
-                tmax = fmaxf(tmax, sc[blk][v]);
-            }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        const float mn = fmaxf(m, tmax);  // finite: row t0 of the tile is in range
-        const float alpha = exp2f(m - mn);  // 0 while m is -inf
-        m = mn;
-        float ps = 0.f;
-        float pr[4][4];
-#pragma unroll
-        for (int blk = 0; blk < 4; ++blk)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const float p = exp2f(sc[blk][v] - mn);  // 0 for masked rows
-                pr[blk][v] = p;
-                ps += p;
-            }
-        l = l * alpha + ps;
-#pragma unroll
-        for (int db = 0; db < DB; ++db) o[db] *= alpha;
-        // O^T += V^T . P^T over rows 32j .. 32j+31: the lane's P slots s = 0..3 are block 2j,
-        // s = 4..7 block 2j+1 — rows 32j + 8lg + s, the rows of its V^T operand
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            float pv[8];
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                pv[v] = pr[2 * j][v];
-                pv[4 + v] = pr[2 * j + 1][v];
-            }
-            half8 ph, pl;
-            split_hl(pv, ph, pl);
-#pragma unroll
-            for (int db = 0; db < DB; ++db) {
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(T.v[j][db], ph, o[db], 0, 0, 0);
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(T.v[j][db], pl, o[db], 0, 0, 0);
-            }
-        }
-    };
-
-    for (int t = tfirst; t < r1;) {
-        const int t2 = t + step;
-        if constexpr (ST == 2) {
-            if (t2 < r1) load_tile(B, t2);
-            compute(A, t);
-            if (t2 >= r1) break;
-            const int t3 = t2 + step;
-            if (t3 < r1) load_tile(A, t3);
-            compute(B, t2);
-            t = t3;
-        } else {
-            compute(A, t);
-            if (t2 < r1) load_tile(A, t2);
-            t = t2;
-        }
-    }
+    aw.run(qh, ql, m, l, o);
 
     // combine the waves: log-sum-exp weights, summed in wave order
     l += __shfl_xor(l, 16);
@@ -602,6 +635,86 @@ __global__ void __launch_bounds__(64 * NW) k_attn_mf(const AttnArgs a) {
     if (threadIdx.x == 0) __hip_atomic_store(&a.cnt[bh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Prefill: one workgroup of NW waves per (16 consecutive query tokens of one sequence, query
+// head); the tokens are the MFMA columns, each masked at its causal limit pos + 1
+// (flash_attention_cpu, cpu_engine.rs:1151-1272: kv_len = start_pos + b + 1). K/V rows are
+// shared by the 16 tokens, so the cache is read once per 16 queries of a head.
+template <int HD, int NW>
+__global__ void __launch_bounds__(64 * NW) k_attn_pf(const AttnArgs a) {
+    constexpr int KC = HD / 32, DB = HD / 16, NT = 64 * NW;
+    __shared__ float q_s[16][HD];
+    __shared__ float w_m[NW][16], w_l[NW][16];
+    __shared__ float w_o[NW][16][HD + 4];
+
+    const int t0 = blockIdx.x * 16, hq = blockIdx.y;
+    const int h = hq / (a.nq / a.nkv);
+    const int ntok = min(16, a.batch - t0);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lr = lane & 15, lg = lane >> 4;
+
+    constexpr int QPT = 16 * HD / NT;
+    float qreg[QPT];
+#pragma unroll
+    for (int k = 0; k < QPT; ++k) {
+        const int i = threadIdx.x + k * NT;
+        qreg[k] = i / HD < ntok ? a.q[((int64_t)(t0 + i / HD) * a.nq + hq) * HD + i % HD] : 0.f;
+    }
+    const int64_t off = a.boff[0];  // one sequence per launch
+    int lim = 0;
+    if (lr < ntok) {
+        lim = a.pos[t0 + lr] + 1;
+        if (a.kv.max_context > 0) lim = min(lim, a.kv.max_context);
+    }
+    int r1 = lim;
+#pragma unroll
+    for (int sh = 8; sh > 0; sh >>= 1) r1 = max(r1, __shfl_xor(r1, sh));
+    const __half* Kc = (const __half*)a.kv.k + ((int64_t)h * a.kv.kv_rows + off) * HD;
+    const __half* Vt = (const __half*)a.kv.v + (int64_t)h * HD * a.kv.kv_rows + off;
+    AttnWave<HD, NW, true> aw{Kc, Vt, a.kv.kv_rows, ((off | a.kv.kv_rows) & 7) == 0, 0, r1, lim};
+    aw.start();
+
+#pragma unroll
+    for (int k = 0; k < QPT; ++k) {
+        const int i = threadIdx.x + k * NT;
+        q_s[i / HD][i % HD] = qreg[k];
+    }
+    __syncthreads();
+    half8 qh[KC], ql[KC];
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) split_hl(&q_s[lr][kc * 32 + 8 * lg], qh[kc], ql[kc]);
+    float m = -INFINITY, l = 0.f;
+    f32x4 o[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    aw.run(qh, ql, m, l, o);
+
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if (lg == 0) {
+        w_m[wave][lr] = m;
+        w_l[wave][lr] = l;
+    }
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) w_o[wave][lr][db * 16 + 4 * lg + v] = o[db][v];
+    __syncthreads();
+    for (int i = threadIdx.x; i < ntok * HD; i += NT) {
+        const int c = i / HD, d = i % HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, w_m[w][c]);
+        float L = 0.f, O = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const float f = w_m[w][c] == -INFINITY ? 0.f : exp2f(w_m[w][c] - M);
+            L += w_l[w][c] * f;
+            O += w_o[w][c][d] * f;
+        }
+        a.out[((int64_t)(t0 + c) * a.nq + hq) * HD + d] = L > 0.f ? O * (1.0f / L) : 0.f;
+    }
+}
+
 template <int HD, int KVF16, int G>
 hipError_t launch_t(const AttnArgs& a, hipStream_t st) {
     if constexpr (KVF16) {
@@ -655,8 +768,15 @@ bool attn_supported(int nq, int nkv, int hd) {
 }
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
-    if (!attn_supported(a.nq, a.nkv, a.hd) || a.splits > MAX_SPLITS || (a.splits > 1 && !a.cnt))
-        return hipErrorInvalidValue;
+    if (!attn_supported(a.nq, a.nkv, a.hd)) return hipErrorInvalidValue;
+    if (a.prefill && a.kv.kv_f16) {
+        if (a.batch <= 0 || !a.pos || !a.boff) return hipErrorInvalidValue;
+        const dim3 grid((a.batch + 15) / 16, a.nq);
+        if (a.hd == 64) launch_kernel((k_attn_pf<64, 4>), grid, dim3(256), 0, st, a);
+        else launch_kernel((k_attn_pf<128, 4>), grid, dim3(256), 0, st, a);
+        return hipGetLastError();
+    }
+    if (a.splits > MAX_SPLITS || (a.splits > 1 && !a.cnt)) return hipErrorInvalidValue;
     if (a.hd == 64) return a.kv.kv_f16 ? launch_g<64, 1>(a, st) : launch_g<64, 0>(a, st);
     return a.kv.kv_f16 ? launch_g<128, 1>(a, st) : launch_g<128, 0>(a, st);
 }

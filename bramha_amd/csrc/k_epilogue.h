@@ -106,7 +106,7 @@ __device__ __forceinline__ void run_epilogue(const GemvArgs& a, const float* fin
         }
     } else if constexpr (EPI == EPI_RESNORM) {
         // residual add (cpu_engine.rs:2937-2939, 2966-2968), then the next norm's inputs
-        static_assert(ROWS == 64, "one sum of squares per 64-row tile");
+        static_assert(ROWS % 64 == 0, "one sum of squares per 64-row tile");
         for (int i = threadIdx.x; i < B * ROWS; i += blockDim.x) {
             const int b = i / ROWS, rr = i % ROWS;
             const int64_t nn = row0 + rr;
@@ -123,10 +123,12 @@ __device__ __forceinline__ void run_epilogue(const GemvArgs& a, const float* fin
             scratch[i] = sq;
         }
         __syncthreads();
-        const int64_t tile = row0 / 64;
-        for (int b = wave; b < B; b += nwaves) {
-            const float t = wave_sum64(scratch[b * ROWS + lane]);
-            if (lane == 0 && b < a.batch) a.ssq_out[(int64_t)b * a.ssq_tiles + tile] = t;
+        constexpr int SUB = ROWS / 64;
+        for (int q = wave; q < B * SUB; q += nwaves) {
+            const int b = q / SUB, sub = q % SUB;
+            const float t = wave_sum64(scratch[b * ROWS + sub * 64 + lane]);
+            const int64_t tile = row0 / 64 + sub;
+            if (lane == 0 && b < a.batch && tile < a.ssq_tiles) a.ssq_out[(int64_t)b * a.ssq_tiles + tile] = t;
         }
     } else if constexpr (EPI == EPI_SILU) {
         for (int i = threadIdx.x; i < B * ROWS; i += blockDim.x) {

@@ -303,21 +303,16 @@ hipError_t launch_gemv(int fmt, int epi, const GemvArgs& a0, hipStream_t st) {
     int b0 = 0;
     while (b0 < a0.batch) {
         const int rem = a0.batch - b0;
-        const bool mf = (fmt == BH_Q4_G32 || fmt == BH_Q4_ROW) && rem >= 16;
+        const bool q4 = fmt == BH_Q4_G32 || fmt == BH_Q4_ROW;
+        if (q4 && rem >= PF_MIN_TOKENS && epi != EPI_LMHEAD) {
+            // prefill chunk: every remaining token in one tiled launch
+            GemvArgs a = gemv_tokens(a0, b0, rem);
+            a.ksw = 1;
+            return launch_gemm_pf(fmt, epi, a, st);
+        }
+        const bool mf = q4 && rem >= 16;
         const int B = mf ? (rem >= 32 ? 32 : 16) : (rem >= 8 ? 8 : (rem >= 4 ? 4 : (rem >= 2 ? 2 : 1)));
-        GemvArgs a = a0;
-        a.batch = B;
-        a.x = a0.x + (int64_t)b0 * a0.ldx;
-        a.y = a0.y + (int64_t)b0 * a0.ldy;
-        if (a0.xw_out) a.xw_out = a0.xw_out + (int64_t)b0 * a0.ldy;
-        if (a0.ssq_in) a.ssq_in = a0.ssq_in + (int64_t)b0 * a0.ssq_tiles;
-        if (a0.ssq_out) a.ssq_out = a0.ssq_out + (int64_t)b0 * a0.ssq_tiles;
-        if (a0.pos) a.pos = a0.pos + b0;
-        if (a0.boff) a.boff = a0.boff + b0;
-        if (a0.slot) a.slot = a0.slot + b0;
-        const int tiles64 = (a0.n_pad + 63) / 64;
-        if (a0.part_val) a.part_val = a0.part_val + (int64_t)b0 * tiles64;
-        if (a0.part_idx) a.part_idx = a0.part_idx + (int64_t)b0 * tiles64;
+        GemvArgs a = gemv_tokens(a0, b0, B);
         hipError_t e;
         if (mf) {
             a.ksw = auto_splits(a0, true, 64 * rw, nacc * B * 64 * rw);

@@ -109,6 +109,26 @@ def test_tiny_fp16_kv(plane):
     assert np.max(np.abs(olg[:n] - glg[:n])) < 2e-2 and max(rel_l2(glg[t], olg[t]) for t in range(n)) < 1e-3
 
 
+@pytest.mark.parametrize("hd128", [False, True])
+def test_tiny_prefill_tiled_fp16_kv(plane, hd128):
+    """A 199-token prefill chunk: tiled MFMA projections over all tokens (QKV with RoPE and KV
+    append, O and down with the residual add, gate/up with SiLU) and the causal prefill
+    attention over the fp16 cache; then decode. head_dim 128 also takes the two-group QKV
+    tiles and the 128-wide attention of the decode steps."""
+    if hd128:
+        cfg = tiny_cfg(Q4_G32, Q4_G32, kv_f16=True, max_tokens=256, hidden=512, n_heads=4, n_kv_heads=2,
+                       head_dim=128, ffn=768)
+    else:
+        cfg = tiny_cfg(Q4_G32, Q4_G32, gqa7=True, kv_f16=True, max_tokens=256)
+    om, gm = _pair(plane, cfg, seed=31 + hd128)
+    p = prompt(200, cfg.vocab, seed=32)
+    oids, olg = om.generate(p, 12, want_logits=True)
+    gids, glg = gm.generate(p, 12, want_logits=True)
+    n = _margin_ok(oids, gids, olg, glg)
+    assert n >= 1
+    assert np.max(np.abs(olg[:n] - glg[:n])) < 2e-2 and max(rel_l2(glg[t], olg[t]) for t in range(n)) < 1e-3
+
+
 def test_ragged_batch_and_refill(plane):
     cfg = tiny_cfg(Q8_ROW, F32, gqa7=True, max_seqs=6)
     om, gm = _pair(plane, cfg, seed=9)

@@ -80,6 +80,18 @@ def test_gemv_q4g32_qwen_shapes(plane, n, k, batch):
         assert np.max(np.abs(y[0] - yo)) <= 1e-5 * max(1.0, np.abs(yo).max())
 
 
+@pytest.mark.parametrize("fmt", [BH_Q4_G32, BH_Q4_ROW])
+@pytest.mark.parametrize("n,k,batch", [(896, 896, 64), (896, 896, 257), (4864, 896, 130), (896, 4864, 200), (300, 96, 71)])
+def test_gemv_prefill_tiles(plane, fmt, n, k, batch):
+    """Token counts of prefill chunks (>= 64): one tiled MFMA launch over all tokens, with ragged
+    row and token tiles."""
+    w = _w(fmt * 17 + n + batch, n, k)
+    q, s, deq = _quant(fmt, w)
+    x = np.random.default_rng(batch).standard_normal((batch, k)).astype(np.float32)
+    y = ops.DeviceWeight(plane, fmt, n, k, q, s).gemv(ops.DeviceArray.from_numpy(plane, x)).numpy()
+    _check_gemv(y, deq, x)
+
+
 @pytest.mark.parametrize("fmt", [BH_F32, BH_Q8_ROW, BH_Q4_ROW])
 @pytest.mark.parametrize("n,k,batch", [(896, 896, 1), (4864, 896, 3), (896, 4864, 8), (300, 96, 5), (896, 4864, 20)])
 def test_gemv_row_formats(plane, fmt, n, k, batch):
