@@ -146,6 +146,132 @@ def attn_sweep(plane, rotate=1 << 30, iters=32, seed=0):
     return out
 
 
+def ragged_decode(plane, n_seq=32, lo=128, hi=8192, steps=128, new_prompt=64, chunk=16, seed=0):
+    """Ragged batched decode, Qwen2-0.5B shape, 4-bit: n_seq sequences whose contexts are drawn
+    uniformly from [lo, hi] by seed (random prompt tokens, prefilled into one packed KV buffer at
+    prefix-sum offsets), then `steps` decode steps of the whole batch; a sequence that emits an
+    EOS id is replaced by a new one with a `new_prompt`-token random prompt (prefilled inside
+    the timed loop). Tokens after an EOS within a chunk of steps are not counted."""
+    import numpy as np
+
+    from bramha_amd import BH_Q4_G32, ops
+    from bramha_amd.model import EOS_IDS, QWEN2_0_5B, DecoderConfig, HipDecoder, synth_tokens, synth_weights
+
+    rng = np.random.default_rng(seed)
+    ctx = rng.integers(lo, hi + 1, size=n_seq)
+    caps = [int(c) + steps + 16 for c in ctx]
+    rep_cap = new_prompt + steps + 16
+    kv_rows = sum((c + 7) // 8 * 8 for c in caps) + n_seq * ((rep_cap + 7) // 8 * 8)
+    cfg = DecoderConfig(**QWEN2_0_5B, wfmt=BH_Q4_G32, head_fmt=BH_Q4_G32, kv_f16=True, max_seqs=2 * n_seq,
+                        kv_rows=kv_rows, max_tokens=2048)
+    m = HipDecoder(plane, cfg)
+    m.load(synth_weights(cfg, seed=seed))
+    firsts = []
+    ops.synchronize(plane)
+    t0 = time.perf_counter()
+    for s in range(n_seq):
+        p = synth_tokens(seed, "ragged.%d" % s, int(ctx[s]), cfg.vocab)
+        m.seq_open(s, caps[s])
+        m.prefill(s, p[:-1])
+        firsts.append(int(p[-1]))
+    ops.synchronize(plane)
+    t_pf = time.perf_counter() - t0
+    pf_tokens = int(ctx.sum()) - n_seq
+    log("ragged: prefilled %d tokens of %d sequences in %.2f s (%.0f tok/s)" % (pf_tokens, n_seq, t_pf, pf_tokens / t_pf))
+    m.decode_setup(np.arange(n_seq, dtype=np.int32), np.array(firsts, np.uint32))
+    m.decode(2)  # graph capture and first replays, untimed
+    ops.synchronize(plane)
+    next_slot, replaced, valid = n_seq, 0, 0
+    t0 = time.perf_counter()
+    done = 0
+    while done < steps:
+        k = min(chunk, steps - done)
+        ids = m.decode(k)
+        for b in range(n_seq):
+            col = ids[:, b]
+            hit = np.nonzero(np.isin(col, EOS_IDS))[0]
+            if hit.size and next_slot < cfg.max_seqs:
+                valid += int(hit[0]) + 1
+                p = synth_tokens(seed, "ragged.new.%d" % next_slot, new_prompt, cfg.vocab)
+                m.seq_open(next_slot, rep_cap)
+                m.prefill(next_slot, p[:-1])
+                m.decode_replace(b, next_slot, int(p[-1]))
+                next_slot += 1
+                replaced += 1
+            else:
+                valid += k
+        done += k
+    ops.synchronize(plane)
+    dt = time.perf_counter() - t0
+    m.close()
+    r = {"value": valid / dt, "unit": "tok/s", "batch": n_seq, "steps": steps, "ms_per_step": dt * 1e3 / steps,
+         "contexts": {"min": int(ctx.min()), "max": int(ctx.max()), "mean": float(ctx.mean())},
+         "replaced": replaced, "prefill_tok_s": pf_tokens / t_pf, "prefill_tokens": pf_tokens}
+    log("ragged: %.1f tok/s decode (%.3f ms/step), %d replaced" % (r["value"], r["ms_per_step"], replaced))
+    return r
+
+
+def qwen7b(plane, prompt_len=2048, steps=256, warmup=8, batches=(1, 16), seed=0):
+    """Qwen2-7B shape, 4-bit g32 (untied LM head), fp16 KV: a prefill of `prompt_len` random
+    tokens (one chunk), then `steps` greedy decode steps at each batch size (each sequence with
+    its own prefilled prompt)."""
+    import numpy as np
+
+    from bramha_amd import BH_Q4_G32, ops
+    from bramha_amd.model import QWEN2_7B, DecoderConfig, HipDecoder, synth_tokens, synth_weights
+
+    nb = max(batches)
+    cap = prompt_len + warmup + steps + 16
+    cfg = DecoderConfig(**QWEN2_7B, wfmt=BH_Q4_G32, head_fmt=BH_Q4_G32, kv_f16=True, max_seqs=1 + nb,
+                        kv_rows=(1 + nb) * ((cap + 7) // 8 * 8), max_tokens=prompt_len, tied=False)
+    m = HipDecoder(plane, cfg)
+    t0 = time.perf_counter()
+
+    def progress(ws):
+        for i, w in enumerate(ws):
+            if i % 40 == 0:
+                log("7b: tensor %d (%s) at %.1f s" % (i, w[0], time.perf_counter() - t0))
+            yield w
+
+    m.load(progress(synth_weights(cfg, seed=seed)))
+    log("7b: weights ready in %.1f s" % (time.perf_counter() - t0))
+    H, I, L, V = cfg.hidden, cfg.ffn, cfg.n_layers, cfg.vocab
+    params = L * (H * (cfg.q_dim + 2 * cfg.kv_dim) + cfg.q_dim * H + 3 * H * I)
+    out = {"params_per_token": params}
+    slot = 0
+    firsts = {}
+    for B in batches:
+        slots = list(range(slot, slot + B))
+        tp = 0.0
+        for s in slots:
+            p = synth_tokens(seed, "7b.prompt.%d" % s, prompt_len, V)
+            m.seq_open(s, cap)
+            ops.synchronize(plane)
+            t0 = time.perf_counter()
+            m.prefill(s, p[:-1])
+            ops.synchronize(plane)
+            tp += time.perf_counter() - t0
+            firsts[s] = int(p[-1])
+        if B == batches[0]:
+            n = prompt_len - 1
+            flops = 2.0 * params * n + 4.0 * L * cfg.n_heads * cfg.head_dim * n * (n + 1) / 2
+            out["prefill"] = {"tokens": n, "seconds": tp / B, "tok_s": n * B / tp, "TFLOPs": flops * B / tp / 1e12,
+                              "mfma_frac": flops * B / tp / 2.5e15}
+            log("7b prefill: %d tokens in %.3f s (%.0f tok/s, %.1f TFLOP/s algorithmic)" %
+                (n, tp / B, n * B / tp, flops * B / tp / 1e12))
+        m.decode_setup(np.array(slots, np.int32), np.array([firsts[s] for s in slots], np.uint32))
+        dt = timed_decode(m, steps, warmup)
+        t = m.time_kernels(8)
+        out["decode_bs%d" % B] = {"tok_s": B * steps / dt, "ms_per_step": dt * 1e3 / steps,
+                                  "weight_GBps": (params + V * H) * 0.5625 / (dt / steps) / 1e9,
+                                  "per_class_us": {k: round(v[0], 2) for k, v in t.items()}}
+        log("7b bs%d per-kernel us: %s" % (B, out["decode_bs%d" % B]["per_class_us"]))
+        log("7b decode bs%d: %.1f tok/s (%.3f ms/step)" % (B, B * steps / dt, dt * 1e3 / steps))
+        slot += B
+    m.close()
+    return out
+
+
 def cpu_baseline(budget_s=15.0, max_steps=64):
     """The reference CPU path (the oracle's restatement of generate_cpu with CPU-only mode):
     Qwen2-0.5B shape, 4-bit per-row projections (the reference's U4 format) and the f32 tied
@@ -183,6 +309,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-bs1", action="store_true")
     ap.add_argument("--no-sweeps", action="store_true", help="skip the isolated GEMV and attention sweeps")
+    ap.add_argument("--full", action="store_true",
+                    help="also run the ragged 32-sequence decode and the Qwen2-7B prefill + decode workloads")
+    ap.add_argument("--only-full", action="store_true", help="run only the --full workloads")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -194,6 +323,10 @@ def main():
     from bramha_amd.plane import HipComputePlane
 
     plane = HipComputePlane(0)
+    if args.only_full:
+        print(json.dumps({"ragged32": ragged_decode(plane), "qwen2_7b": qwen7b(plane)}), flush=True)
+        plane.close()
+        return
     total = args.warmup + args.steps
     log("building bs1 model")
     m1, cfg = build_model(plane, 1, args.prompt, total + 32)
@@ -220,6 +353,9 @@ def main():
         gsweep = gemv_sweep(plane)
         log("isolated attention sweep")
         asweep = attn_sweep(plane)
+    full = None
+    if args.full:
+        full = {"ragged32": ragged_decode(plane), "qwen2_7b": qwen7b(plane)}
     cpu = None
     if not args.no_cpu_baseline:
         log("timing the CPU baseline")
@@ -247,6 +383,7 @@ def main():
         "cpu_baseline": cpu,
         "gemv_sweep": gsweep,
         "attn_sweep": asweep,
+        "full": full,
     }
     print(json.dumps(line), flush=True)
     plane.close()

@@ -65,6 +65,12 @@ int bh_ctx::ensure_scratch(size_t xb, size_t yb) {
     return BH_OK;
 }
 
+void bh_ctx::split_scratch(bh::GemvArgs& a, hipStream_t st) {
+    if (st != stream || !split_part) return;
+    a.part = split_part;
+    a.tile_cnt = split_cnt;
+}
+
 namespace bh {
 
 void free_weight(DevWeight& w) {
@@ -303,6 +309,16 @@ int bh_init(int device, bh_ctx** out) {
         delete c;
         return BH_ERR_HIP;
     }
+    // split scratch up front, so that no GEMV call (captured or not) allocates
+    const size_t pb = (size_t)SPLIT_WG_MAX * SPLIT_TOT_MAX * 4, cb = (size_t)SPLIT_WG_MAX * 4;
+    if (hipMalloc(&c->split_part, pb) != hipSuccess || hipMalloc(&c->split_cnt, cb) != hipSuccess ||
+        hipMemset(c->split_cnt, 0, cb) != hipSuccess) {
+        if (c->split_part) hipFree(c->split_part);
+        if (c->split_cnt) hipFree(c->split_cnt);
+        hipStreamDestroy(c->stream);
+        delete c;
+        return BH_ERR_OOM;
+    }
     *out = c;
     return BH_OK;
 }
@@ -317,6 +333,8 @@ void bh_destroy(bh_ctx* ctx) {
     for (auto& kv : ctx->rope_tabs) hipFree(kv.second);
     if (ctx->attn_part) hipFree(ctx->attn_part);
     if (ctx->attn_cnt) hipFree(ctx->attn_cnt);
+    if (ctx->split_part) hipFree(ctx->split_part);
+    if (ctx->split_cnt) hipFree(ctx->split_cnt);
     hipStreamDestroy(ctx->stream);
     delete ctx;
 }
@@ -465,7 +483,9 @@ int bh_gemv(bh_ctx* ctx, const bh_weight* wh, const float* x, float* y, int batc
     a.n_pad = (int)w->n_pad;
     a.C = (int)w->chunks;
     a.batch = batch;
-    hipError_t e = launch_gemv(w->fmt, EPI_STORE, a, pick(ctx, stream));
+    const hipStream_t hs = pick(ctx, stream);
+    ctx->split_scratch(a, hs);
+    hipError_t e = launch_gemv(w->fmt, EPI_STORE, a, hs);
     return e == hipSuccess ? BH_OK : ctx->hip_fail(e, "gemv launch");
 }
 
@@ -659,6 +679,7 @@ int bh_time_gemv(bh_ctx* ctx, const bh_weight* wh, const float* x, float* y, int
             a.n_pad = (int)c.n_pad;
             a.C = (int)c.chunks;
             a.batch = batch;
+            ctx->split_scratch(a, st);
             return launch_gemv(c.fmt, EPI_STORE, a, st);
         }, us_per_launch);
     for (int i = 1; i < copies; ++i) {

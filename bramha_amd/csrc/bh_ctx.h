@@ -36,6 +36,10 @@ struct bh_ctx {
     int32_t* attn_cnt = nullptr;  // split-merge counters, zero when idle
     int attn_cnt_len = 0;
     std::unordered_map<std::string, void*> rope_tabs;
+    // K-split scratch of the GEMVs launched on the context's own stream (split sums and arrival
+    // counters, zero when idle); calls on other streams run unsplit so they never share it.
+    float* split_part = nullptr;
+    int32_t* split_cnt = nullptr;
 
     // Fault injection (bh_debug_inject_fault).
     int inj_op = 0, inj_status = 0, inj_count = 0;
@@ -44,6 +48,8 @@ struct bh_ctx {
     int hip_fail(hipError_t e, const char* what);
     bool injected(int op, int* status);
     int ensure_scratch(size_t xb, size_t yb);
+    // Point a's split scratch at the context's when `st` is the context's stream.
+    void split_scratch(bh::GemvArgs& a, hipStream_t st);
     void touch(const std::string& key);
     void enforce_limits(size_t new_bytes);
     void clear_registry();

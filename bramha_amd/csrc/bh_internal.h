@@ -156,7 +156,7 @@ hipError_t launch_gemm_mf(int fmt, int epi, const GemvArgs& a, int B, int rw, hi
 hipError_t launch_gemm_pf(int fmt, int epi, const GemvArgs& a, hipStream_t st);
 constexpr int PF_MIN_TOKENS = 64;  // launch_gemv hands passes of at least this many tokens to it
 // Workgroups per row tile for a K-split GEMV over `tiles` row tiles and C chunks.
-int gemv_splits(int tiles, int C, int min_chunks);
+int gemv_splits(int tiles, int C, int min_chunks, int target);
 constexpr int MAX_KSW = 16;
 // Cache policy of buffer loads for data read once per launch (weights): non-temporal. Used for
 // weights of at least STREAM_BYTES packed bytes.

@@ -50,6 +50,8 @@ struct bh_model {
     std::vector<LayerW> L;
     DevWeight embed;
     bool have_embed = false;
+    DevWeight lm_head;  // untied LM head ("lm_head.weight"); the embedding when absent
+    bool have_lm_head = false;
     float* norm = nullptr;
     bool have_norm = false;
 
@@ -63,6 +65,7 @@ struct bh_model {
     float* attn_part = nullptr;
     int max_splits = 128;
     int32_t* attn_cnt = nullptr;   // [max_tokens][n_kv] split-merge counters
+    size_t attn_rows = 0;          // query rows of attn_part
     float* split_part = nullptr;   // K-split sums of split projections
     int32_t* split_cnt = nullptr;  // their per-tile arrival counters (zero when idle)
     // decode batch state (read by the captured graph) and prefill staging, kept apart so a
@@ -218,7 +221,7 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
         at.splits = splits;
         at.split_rows = split_rows;
         at.part_o = m->attn_part;
-        at.part_ml = m->attn_part + (size_t)c.max_tokens * c.n_heads * m->max_splits * c.head_dim;
+        at.part_ml = m->attn_part + m->attn_rows * c.n_heads * m->max_splits * c.head_dim;
         at.cnt = m->attn_cnt;
         at.prefill = decode ? 0 : 1;
         e = timed(m, BH_K_ATTN, [&] { return launch_attention(at, st); });
@@ -252,7 +255,7 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
     }
     if (e != hipSuccess || !decode) return e;
     GemvArgs lm;
-    weight_args(m, lm, m->embed);
+    weight_args(m, lm, m->have_lm_head ? m->lm_head : m->embed);
     stream_input(m, lm);
     lm.y = m->logits;
     lm.ldy = c.vocab;
@@ -428,6 +431,10 @@ int bh_model_create(bh_ctx* ctx, const bh_model_config* cfg, bh_model** out) {
         if ((e = dmalloc(m, &m->vc[l], kvb)) != hipSuccess) return bail(e, "hipMalloc(V cache)");
     }
     const size_t T = (size_t)c.max_tokens;
+    // decode-only buffers hold one row per batch entry (at most one entry per slot); the split
+    // partials also serve f32-cache prefill chunks (one query per token)
+    const size_t DB = std::min<size_t>(T, (size_t)c.max_seqs);
+    m->attn_rows = c.kv_f16 ? DB : T;
     struct {
         void** p;
         size_t bytes;
@@ -438,10 +445,10 @@ int bh_model_create(bh_ctx* ctx, const bh_model_config* cfg, bh_model** out) {
         {(void**)&m->q, T * QD * 4},
         {(void**)&m->att, T * QD * 4},
         {(void**)&m->mm, T * c.ffn * 4},
-        {(void**)&m->logits, T * c.vocab * 4},
-        {(void**)&m->part_val, T * m->tiles_lm * 4},
-        {(void**)&m->part_idx, T * m->tiles_lm * 4},
-        {(void**)&m->attn_part, T * c.n_heads * m->max_splits * (c.head_dim + 2) * 4},
+        {(void**)&m->logits, DB * c.vocab * 4},
+        {(void**)&m->part_val, DB * m->tiles_lm * 4},
+        {(void**)&m->part_idx, DB * m->tiles_lm * 4},
+        {(void**)&m->attn_part, m->attn_rows * c.n_heads * m->max_splits * (c.head_dim + 2) * 4},
         {(void**)&m->attn_cnt, T * c.n_kv_heads * 4},
         {(void**)&m->split_part, (size_t)SPLIT_WG_MAX * SPLIT_TOT_MAX * 4},
         {(void**)&m->split_cnt, (size_t)4096 * 4},
@@ -454,7 +461,7 @@ int bh_model_create(bh_ctx* ctx, const bh_model_config* cfg, bh_model** out) {
         {(void**)&m->d_ppos, T * 4},
         {(void**)&m->d_pslot, T * 4},
         {(void**)&m->d_pboff, T * 8},
-        {(void**)&m->d_ids, (size_t)m->ids_steps * T * 4},
+        {(void**)&m->d_ids, (size_t)m->ids_steps * DB * 4},
         {(void**)&m->d_pen, (size_t)c.max_seqs * c.vocab * 2},
     };
     for (auto& b : bufs)
@@ -486,6 +493,7 @@ void bh_model_destroy(bh_model* m) {
         free_weight(w.down);
     }
     free_weight(m->embed);
+    free_weight(m->lm_head);
     for (void* p : m->allocs) hipFree(p);
     for (auto& ev : m->ev_pool) {
         hipEventDestroy(ev.start);
@@ -508,6 +516,12 @@ int bh_model_set_weight(bh_model* m, const char* name, const void* data, size_t 
         int rc = ensure_weight(m, m->embed, c.head_fmt, c.vocab, H);
         if (!rc) rc = upload_rows(m->ctx, m->embed, 0, c.vocab, data, bytes, scales, scale_bytes);
         if (!rc) m->have_embed = true;
+        return rc;
+    }
+    if (!std::strcmp(name, "lm_head.weight")) {  // optional: cpu_engine.rs:2449-2451 falls back to the embedding
+        int rc = ensure_weight(m, m->lm_head, c.head_fmt, c.vocab, H);
+        if (!rc) rc = upload_rows(m->ctx, m->lm_head, 0, c.vocab, data, bytes, scales, scale_bytes);
+        if (!rc) m->have_lm_head = true;
         return rc;
     }
     if (!std::strcmp(name, "model.norm.weight")) {
@@ -655,7 +669,8 @@ static hipError_t set_entry(bh_model* m, int b, int slot, uint32_t token) {
 int bh_model_decode_setup(bh_model* m, int batch, const int32_t* slots, const uint32_t* first_tokens) {
     if (!m || batch <= 0 || !slots || !first_tokens) return BH_ERR_INVALID;
     std::lock_guard<std::mutex> g(m->ctx->mu);
-    if (batch > m->c.max_tokens) return m->fail(BH_ERR_CAPACITY, "decode batch above max_tokens");
+    if (batch > m->c.max_tokens || batch > m->c.max_seqs)
+        return m->fail(BH_ERR_CAPACITY, "decode batch above max_tokens or max_seqs");
     std::vector<int32_t> seen(m->c.max_seqs, 0);
     for (int b = 0; b < batch; ++b) {
         if (slots[b] < 0 || slots[b] >= m->c.max_seqs || !m->open_h[slots[b]])
@@ -838,7 +853,7 @@ int bh_model_kernel_bytes(bh_model* m, int kclass, double* bytes) {
         case BH_K_GEMV_GATEUP: *bytes = weight_bytes(w.gate) + weight_bytes(w.up) + B * (H + T) * 4 + B * I * 4; return BH_OK;
         case BH_K_GEMV_DOWN: *bytes = weight_bytes(w.down) + B * I * 4 + B * (3 * H + T) * 4 + H * 4; return BH_OK;
         case BH_K_LM_HEAD:  // tied table, xw in; logits out, penalty counts read
-            *bytes = weight_bytes(m->embed) + B * (H + T) * 4 + B * (double)c.vocab * 4 + B * (double)c.vocab * 2;
+            *bytes = weight_bytes(m->have_lm_head ? m->lm_head : m->embed) + B * (H + T) * 4 + B * (double)c.vocab * 4 + B * (double)c.vocab * 2;
             return BH_OK;
         case BH_K_ATTN: {
             double rows = 0;

@@ -262,15 +262,18 @@ hipError_t launch_fmt(int epi, const GemvArgs& a, int B, int rw, int ksplit, int
 // 3.5 TB/s where 1 wave per tile streams 2.8.)
 static int waves_per_tile(int tiles, int rw, int C, int nacc, int B) {
     int ks = (8192 + tiles * rw - 1) / (tiles * rw);
-    ks = std::max(1, std::min({ks, 16 / rw, std::max(1, C / 2)}));
+    // at most 12 waves per tile on matrices with many row tiles (two 768-thread workgroups per CU
+    // stay resident: 18944 x 3584 streams 2.8 TB/s instead of 2.3 with 16), 16 on small ones
+    // (latency-bound: 16 waves per tile are fastest on 4864 x 896)
+    ks = std::max(1, std::min({ks, (tiles > 128 ? 12 : 16) / rw, std::max(1, C / 2)}));
     while (ks > 1 && (size_t)ks * nacc * B * 64 * rw * 4 > 60 * 1024) --ks;
     return ks;
 }
 
-// Workgroups per row tile for a K-split GEMV: enough for about one workgroup per CU (256),
-// each streaming at least `min_chunks` chunks, at most MAX_KSW.
-int gemv_splits(int tiles, int C, int min_chunks) {
-    const int ksw = 256 / std::max(tiles, 1);
+// Workgroups per row tile for a K-split GEMV: about `target` workgroups in all, each streaming
+// at least `min_chunks` chunks, at most MAX_KSW.
+int gemv_splits(int tiles, int C, int min_chunks, int target) {
+    const int ksw = target / std::max(tiles, 1);
     return std::max(1, std::min({ksw, MAX_KSW, std::max(1, C / std::max(min_chunks, 1))}));
 }
 
@@ -283,9 +286,13 @@ static int auto_splits(const GemvArgs& a, bool mfma, int rows_per_tile, int tot)
     if (!a.part || !a.tile_cnt || tot > SPLIT_TOT_MAX) return 1;
     const int tiles = (a.n_pad + rows_per_tile - 1) / rows_per_tile;
     int ksw;
-    // splits pay for their ordered reduction only on long-K matrices with few row tiles (measured:
-    // the 896-wide projections are fastest unsplit at 1 and at 32 tokens)
-    ksw = (tiles <= 32 && a.C >= 64) ? std::min(gemv_splits(tiles, a.C, 8), mfma ? 16 : 8) : 1;
+    // splits pay for their ordered reduction only on long-K matrices (measured: the 896-wide
+    // projections are fastest unsplit at 1 and at 32 tokens; the 3584- and 18944-wide ones of a
+    // 7B model stream 1.3-2x faster split to fill the CUs); MFMA passes aim at two workgroups
+    // per CU, VALU passes at one
+    ksw = !(a.C >= 64) ? 1
+          : mfma ? (tiles < 256 ? gemv_splits(tiles, a.C, 16, 512) : 1)
+                 : (tiles < 128 ? std::min(gemv_splits(tiles, a.C, 16, 256), 8) : 1);
     while (ksw > 1 && tiles * ksw > SPLIT_WG_MAX) --ksw;
     return ksw;
 }

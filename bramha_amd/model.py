@@ -41,6 +41,7 @@ class DecoderConfig:
     max_seqs: int = 1
     kv_rows: int = 4096
     max_tokens: int = 64
+    tied: bool = True  # False: a separate "lm_head.weight" (host-side only: the C config has no field)
 
     @property
     def q_dim(self):
@@ -53,7 +54,8 @@ class DecoderConfig:
     def to_c(self):
         c = _lib.bh_model_config()
         for k, v in asdict(self).items():
-            setattr(c, k, int(v) if isinstance(v, bool) else v)
+            if k != "tied":
+                setattr(c, k, int(v) if isinstance(v, bool) else v)
         return c
 
 
@@ -61,6 +63,8 @@ def tensor_shapes(cfg):
     """(name, shape) of every tensor, Hugging Face names (tied LM head)."""
     H, I, V = cfg.hidden, cfg.ffn, cfg.vocab
     out = [("model.embed_tokens.weight", (V, H)), ("model.norm.weight", (H,))]
+    if not cfg.tied:
+        out.append(("lm_head.weight", (V, H)))
     for l in range(cfg.n_layers):
         p = "model.layers.%d." % l
         out += [
@@ -122,7 +126,7 @@ def synth_weights(cfg, seed=0, sigma=0.02):
         if len(shape) == 1:
             yield name, w, None
             continue
-        fmt = cfg.head_fmt if name == "model.embed_tokens.weight" else cfg.wfmt
+        fmt = cfg.head_fmt if name in ("model.embed_tokens.weight", "lm_head.weight") else cfg.wfmt
         if fmt == BH_F32:
             yield name, w, None
         else:

@@ -178,7 +178,8 @@ int bh_model_create(bh_ctx* ctx, const bh_model_config* cfg, bh_model** out);
 void bh_model_destroy(bh_model* m);
 /* Upload one tensor by its Hugging Face name from host memory, reference layout:
  * projections in cfg.wfmt (scales as in bh_weight_upload), "model.embed_tokens.weight"
- * in cfg.head_fmt (the LM head is tied to it), norms and biases f32. */
+ * in cfg.head_fmt, norms and biases f32. An optional "lm_head.weight" (cfg.head_fmt) unties the
+ * LM head; without it the head is the embedding (cpu_engine.rs:2449-2455). */
 int bh_model_set_weight(bh_model* m, const char* name, const void* data, size_t bytes, const void* scales,
                         size_t scale_bytes);
 /* Number of tensors still missing (0 when the model can run). */

@@ -507,6 +507,7 @@ struct OrcLayer {
 struct OrcModel {
     orc_config c;
     std::vector<float> embed;  // [V][H] f32 (dequantized when the table is 4-bit)
+    std::vector<float> lm;     // untied LM head [V][H] (empty: the embedding)
     std::vector<float> norm;
     std::vector<OrcLayer> layers;
 };
@@ -592,6 +593,15 @@ int orc_model_set(void* p, const char* name, const void* data, const void* scale
         }
         return 0;
     }
+    if (!std::strcmp(name, "lm_head.weight")) {  // cpu_engine.rs:2449-2455: lm_head, else the embedding
+        if (c.head_fmt == F32) {
+            vec(m->lm, data, V * H);
+        } else {
+            m->lm.resize(V * H);
+            orc_dequantize_q4g32((const uint8_t*)data, (const uint16_t*)scales, V, H, m->lm.data());
+        }
+        return 0;
+    }
     if (!std::strcmp(name, "model.norm.weight")) {
         vec(m->norm, data, H);
         return 0;
@@ -656,7 +666,7 @@ int64_t orc_generate(void* p, const uint32_t* prompt, int64_t n_prompt, int64_t 
     std::vector<uint32_t> tokens(prompt, prompt + n_prompt);
     if (tokens.empty()) tokens.push_back(1);  // :2487-2489
     std::vector<KvCache> kv(NL);
-    const WView lm{F32, m->embed.data(), nullptr, nullptr, nullptr};
+    const WView lm{F32, m->lm.empty() ? m->embed.data() : m->lm.data(), nullptr, nullptr, nullptr};
 
     // ---- prefill ----
     const int64_t pre_end = tokens.size() > 1 ? (int64_t)tokens.size() - 1 : 0;

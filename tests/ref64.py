@@ -165,7 +165,8 @@ class Decoder64:
         gen, logits = [], []
         while len(gen) < max_new:
             x = self._forward(toks[-1], len(toks) - 1, kv)
-            lg = self.t["model.embed_tokens.weight"] @ rms_norm(x, self.t["model.norm.weight"], c.rms_eps)
+            head = self.t.get("lm_head.weight", self.t["model.embed_tokens.weight"])  # cpu_engine.rs:2449-2451
+            lg = head @ rms_norm(x, self.t["model.norm.weight"], c.rms_eps)
             logits.append(lg.copy())
             for g in gen:
                 lg[g] = lg[g] / 1.15 if lg[g] > 0 else lg[g] * 1.15

@@ -129,6 +129,16 @@ def test_tiny_prefill_tiled_fp16_kv(plane, hd128):
     assert np.max(np.abs(olg[:n] - glg[:n])) < 2e-2 and max(rel_l2(glg[t], olg[t]) for t in range(n)) < 1e-3
 
 
+def test_tiny_untied_lm_head(plane):
+    cfg = tiny_cfg(Q4_G32, Q4_G32, gqa7=True, tied=False)
+    om, gm = _pair(plane, cfg, seed=41)
+    p = prompt(9, cfg.vocab, seed=42)
+    oids, olg = om.generate(p, 12, want_logits=True)
+    gids, glg = gm.generate(p, 12, want_logits=True)
+    assert np.array_equal(oids, gids)
+    assert np.max(np.abs(olg - glg)) <= 1e-4 * max(1.0, np.abs(olg).max())
+
+
 def test_ragged_batch_and_refill(plane):
     cfg = tiny_cfg(Q8_ROW, F32, gqa7=True, max_seqs=6)
     om, gm = _pair(plane, cfg, seed=9)

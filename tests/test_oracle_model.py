@@ -28,6 +28,18 @@ def test_oracle_decoder_vs_float64(wfmt, head_fmt):
     assert np.max(np.abs(lg - rlg)) < 2e-4 * max(1.0, np.abs(rlg).max())
 
 
+@pytest.mark.parametrize("head_fmt", [F32, Q4_G32])
+def test_oracle_untied_lm_head(head_fmt):
+    """lm_head.weight present: logits come from it, not the embedding (cpu_engine.rs:2449-2451)."""
+    cfg = tiny_cfg(Q4_G32, head_fmt, tied=False)
+    ids, lg, rids, rlg = _run(cfg, 9, 10, seed=7)
+    assert np.array_equal(ids, rids)
+    assert np.max(np.abs(lg - rlg)) < 2e-4 * max(1.0, np.abs(rlg).max())
+    # the tied model (same seed, same other tensors) gives different logits
+    _, lg2, _, _ = _run(tiny_cfg(Q4_G32, head_fmt), 9, 10, seed=7)
+    assert np.max(np.abs(lg2[0] - lg[0])) > 1e-3
+
+
 def test_oracle_gqa7_and_two_prefill_chunks():
     cfg = tiny_cfg(Q8_ROW, F32, gqa7=True)
     ids, lg, rids, rlg = _run(cfg, 70, 6, seed=3)  # 69 prefill tokens: chunks of 64 + 5

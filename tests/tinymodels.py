@@ -35,7 +35,7 @@ def tiny_weights(cfg, seed=0, sigma=0.05, norm_jitter=True):
             out.append((name, w, None))
             deq[name] = w
             continue
-        fmt = cfg.head_fmt if name == "model.embed_tokens.weight" else cfg.wfmt
+        fmt = cfg.head_fmt if name in ("model.embed_tokens.weight", "lm_head.weight") else cfg.wfmt
         if fmt == F32:
             out.append((name, w, None))
             deq[name] = w
