@@ -115,7 +115,8 @@ def gemv_sweep(plane, rotate=1 << 30, iters=64):
     return out
 
 
-def attn_sweep(plane, rotate=1 << 30, iters=32, seed=0):
+def attn_sweep(plane, rotate=1 << 30, iters=32, seed=0, nq=14, nkv=2, hd=64, contexts=(512, 4096, 32768),
+               batches=(1, 8)):
     """GQA decode attention alone: 14 query heads over 2 KV heads of 64, fp16 K/V N(0, 1) (V
     stored transposed), one query token per sequence at the end of its context, softmax in f32.
     Bytes = K + V rows read + queries + outputs."""
@@ -123,11 +124,10 @@ def attn_sweep(plane, rotate=1 << 30, iters=32, seed=0):
 
     from bramha_amd import ops
 
-    nq, nkv, hd = 14, 2, 64
     rng = np.random.default_rng(seed)
     out = []
-    for T in (512, 4096, 32768):
-        for B in (1, 8):
+    for T in contexts:
+        for B in batches:
             rows = T * B
             k = rng.standard_normal((nkv, rows, hd), dtype=np.float32).astype(np.float16)
             v = rng.standard_normal((nkv, hd, rows), dtype=np.float32).astype(np.float16)

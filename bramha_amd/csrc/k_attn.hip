@@ -308,11 +308,13 @@ __device__ __forceinline__ void split_hl(const float* x, half8& hi, half8& lo) {
 // cover rows 32j .. 32j+31 with row group g = i / 4 owning rows 32j + 8g .. 32j + 8g + 7.
 __device__ __forceinline__ int mf_row(int blk, int i) { return 32 * (blk >> 1) + 8 * (i >> 2) + 4 * (blk & 1) + (i & 3); }
 
-// K and V^T operands of one 64-row tile for one wave.
+// K and V^T operands of one tile of 32 * NJ rows for one wave (NJ = 2 at head_dim 64, 1 at 128:
+// 16 KiB of K + V either way, so two tiles in flight fit the register file).
 template <int HD>
 struct KvTile {
-    half8 k[4][HD / 32];  // S^T A operand: rows mf_row(blk, lr), head-dim kc*32 + 8lg .. +7
-    half8 v[2][HD / 16];  // O^T A operand: head-dim db*16 + lr, rows 32j + 8lg .. +7
+    static constexpr int NJ = HD == 64 ? 2 : 1;
+    half8 k[2 * NJ][HD / 32];  // S^T A operand: rows mf_row(blk, lr), head-dim kc*32 + 8lg .. +7
+    half8 v[NJ][HD / 16];      // O^T A operand: head-dim db*16 + lr, rows 32j + 8lg .. +7
 };
 
 __device__ __forceinline__ unsigned long long ld_agent64(const float* p) {
@@ -323,8 +325,8 @@ __device__ __forceinline__ float2 u64_f2(unsigned long long v) {
 }
 
 // The wave's share of a context range for the 16 query columns held as fp16 hi + lo (qh, ql):
-// 64-row tiles r0 + 64*(wave + NW*i) below r1, with the next tile's K/V loads in flight while
-// the current one is multiplied (two register stages at head_dim 64, one at 128). Row t is
+// tiles of TR rows at r0 + TR*(wave + NW*i) below r1, with the next tile's K/V loads in flight
+// while the current one is multiplied. Row t is
 // valid for the lane's column while t < lim (the causal limit of the column). Scores are kept in
 // the base-2 domain: s2 = (q . k) * log2(e)/sqrt(hd), p = 2^(s2 - m). On return m is the
 // column's running max, l this lane's share of its sum and o its unnormalised output
@@ -335,7 +337,9 @@ template <int HD, int NW, bool MASKCOL>
 struct AttnWave {
     static constexpr int KC = HD / 32;  // 32-wide head-dim chunks of the score product
     static constexpr int DB = HD / 16;  // 16-wide head-dim blocks of the value product
-    static constexpr int ST = HD == 64 ? 2 : 1;
+    static constexpr int NJ = KvTile<HD>::NJ;
+    static constexpr int NB = 2 * NJ;   // 16-row MFMA blocks per tile
+    static constexpr int TR = 32 * NJ;  // rows per tile
     const __half* Kc;
     const __half* Vt;
     int64_t kv_rows;
@@ -347,7 +351,7 @@ struct AttnWave {
         const int lane = threadIdx.x & 63;
         const int lr = lane & 15, lg = lane >> 4;
 #pragma unroll
-        for (int blk = 0; blk < 4; ++blk) {
+        for (int blk = 0; blk < NB; ++blk) {
             const int t = t0 + mf_row(blk, lr);
 #pragma unroll
             for (int kc = 0; kc < KC; ++kc) {
@@ -356,7 +360,7 @@ struct AttnWave {
             }
         }
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < NJ; ++j) {
             const int tg = t0 + 32 * j + 8 * lg;  // this lane group's 8 rows
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
@@ -374,7 +378,7 @@ struct AttnWave {
     }
 
     __device__ __forceinline__ void start() {
-        const int t = r0 + (int)(threadIdx.x >> 6) * 64;
+        const int t = r0 + (int)(threadIdx.x >> 6) * TR;
         if (t < r1) load_tile(A, t);
     }
 
@@ -384,9 +388,9 @@ struct AttnWave {
         const int lg = lane >> 4;
         const float scale2 = 1.4426950408889634f / sqrtf((float)HD);
         // S^T: lane holds rows mf_row(blk, 4lg + v) of column lr
-        f32x4 sc[4];
+        f32x4 sc[NB];
 #pragma unroll
-        for (int blk = 0; blk < 4; ++blk) {
+        for (int blk = 0; blk < NB; ++blk) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kc = 0; kc < KC; ++kc) {
@@ -397,7 +401,7 @@ struct AttnWave {
         }
         float tmax = -INFINITY;
 #pragma unroll
-        for (int blk = 0; blk < 4; ++blk)
+        for (int blk = 0; blk < NB; ++blk)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const bool ok = t0 + mf_row(blk, 4 * lg + v) < lim;
@@ -411,9 +415,9 @@ struct AttnWave {
         if constexpr (MASKCOL) alpha = mn == -INFINITY ? 1.f : alpha;
         m = mn;
         float ps = 0.f;
-        float pr[4][4];
+        float pr[NB][4];
 #pragma unroll
-        for (int blk = 0; blk < 4; ++blk)
+        for (int blk = 0; blk < NB; ++blk)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 float p = exp2f(sc[blk][v] - mn);  // 0 for masked rows
@@ -427,7 +431,7 @@ struct AttnWave {
         // O^T += V^T . P^T over rows 32j .. 32j+31: the lane's P slots s = 0..3 are block 2j,
         // s = 4..7 block 2j+1 — rows 32j + 8lg + s, the rows of its V^T operand
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < NJ; ++j) {
             float pv[8];
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
@@ -445,22 +449,16 @@ struct AttnWave {
     }
 
     __device__ __forceinline__ void run(const half8 (&qh)[KC], const half8 (&ql)[KC], float& m, float& l, f32x4 (&o)[DB]) {
-        const int step = NW * 64;
-        for (int t = r0 + (int)(threadIdx.x >> 6) * 64; t < r1;) {
+        const int step = NW * TR;
+        for (int t = r0 + (int)(threadIdx.x >> 6) * TR; t < r1;) {
             const int t2 = t + step;
-            if constexpr (ST == 2) {
-                if (t2 < r1) load_tile(B, t2);
-                compute(A, t, qh, ql, m, l, o);
-                if (t2 >= r1) break;
-                const int t3 = t2 + step;
-                if (t3 < r1) load_tile(A, t3);
-                compute(B, t2, qh, ql, m, l, o);
-                t = t3;
-            } else {
-                compute(A, t, qh, ql, m, l, o);
-                if (t2 < r1) load_tile(A, t2);
-                t = t2;
-            }
+            if (t2 < r1) load_tile(B, t2);
+            compute(A, t, qh, ql, m, l, o);
+            if (t2 >= r1) break;
+            const int t3 = t2 + step;
+            if (t3 < r1) load_tile(A, t3);
+            compute(B, t2, qh, ql, m, l, o);
+            t = t3;
         }
     }
 };
@@ -756,7 +754,7 @@ void attn_plan(int max_len, int batch, int nkv, int* splits, int* split_rows) {
     int rows = (max_len + want - 1) / want;
     rows = std::max(rows, ATTN_MIN_ROWS);
     rows = std::max(rows, (max_len + MAX_SPLITS - 1) / MAX_SPLITS);
-    rows = (rows + 255) / 256 * 256;
+    rows = (rows + 63) / 64 * 64;
     *splits = (max_len + rows - 1) / rows;
     *split_rows = rows;
 }

@@ -262,10 +262,11 @@ hipError_t launch_fmt(int epi, const GemvArgs& a, int B, int rw, int ksplit, int
 // 3.5 TB/s where 1 wave per tile streams 2.8.)
 static int waves_per_tile(int tiles, int rw, int C, int nacc, int B) {
     int ks = (8192 + tiles * rw - 1) / (tiles * rw);
-    // at most 12 waves per tile on matrices with many row tiles (two 768-thread workgroups per CU
-    // stay resident: 18944 x 3584 streams 2.8 TB/s instead of 2.3 with 16), 16 on small ones
-    // (latency-bound: 16 waves per tile are fastest on 4864 x 896)
-    ks = std::max(1, std::min({ks, (tiles > 128 ? 12 : 16) / rw, std::max(1, C / 2)}));
+    // at most 12 waves per tile (8 for the gate/up pair, whose kernel holds fewer waves per CU) on
+    // matrices with many row tiles, so that every workgroup of the launch stays resident (18944 x
+    // 3584 streams 2.8 TB/s instead of 2.3 with 16; the 7B gate/up pair 25 us instead of 31);
+    // 16 on small ones (latency-bound: 16 waves per tile are fastest on 4864 x 896)
+    ks = std::max(1, std::min({ks, (tiles > 128 ? (nacc == 2 ? 8 : 12) : 16) / rw, std::max(1, C / 2)}));
     while (ks > 1 && (size_t)ks * nacc * B * 64 * rw * 4 > 60 * 1024) --ks;
     return ks;
 }
