@@ -57,7 +57,24 @@ def timed_decode(m, steps, warmup):
     return time.perf_counter() - t0
 
 
-def roofline(m, n_steps=16):
+TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "pmc_traffic_decode_qwen2_0.5b_q4g32_bs1.md")
+
+
+def pmc_traffic(kclass):
+    """HBM bytes per launch of a kernel class at batch 1, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (scaled by its copy probe); None when not measured."""
+    try:
+        for line in open(TRAFFIC_PROFILE):
+            if line.startswith("traffic:"):
+                vals = dict(kv.split("=") for kv in line.split()[1:])
+                return float(vals[kclass]) if kclass in vals else None
+    except OSError:
+        return None
+    return None
+
+
+def roofline(m, n_steps=16, traffic=False):
     """Per-kernel-class mean launch durations over eager decode steps (HIP events on the
     model's stream) and the algorithmic bytes of one launch; the dominant class is the one
     with the largest total time per step."""
@@ -71,7 +88,8 @@ def roofline(m, n_steps=16):
     nbytes = m.kernel_bytes(best)
     achieved = nbytes / (mean_us * 1e-6)
     return best, {"bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                  "frac": achieved / HBM_PEAK, "traffic": None, "kernel": best, "bytes_per_launch": nbytes,
+                  "frac": achieved / HBM_PEAK, "traffic": pmc_traffic(best) if traffic else None, "kernel": best,
+                  "bytes_per_launch": nbytes,
                   "mean_us": mean_us,
                   "per_class_us": {k: round(v[0], 3) for k, v in t.items()},
                   "launches_per_step": {k: v[1] // n_steps for k, v in t.items()}}
@@ -312,6 +330,10 @@ def main():
     ap.add_argument("--full", action="store_true",
                     help="also run the ragged 32-sequence decode and the Qwen2-7B prefill + decode workloads")
     ap.add_argument("--only-full", action="store_true", help="run only the --full workloads")
+    ap.add_argument("--profile-eager", action="store_true",
+                    help="for counter collection: only eager (non-graph) bs1 decode steps, kernel by kernel")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
+                    help="for counter scaling: a plain device copy of MB megabytes (torch), 4 times")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -320,9 +342,27 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
+    if args.copy_probe:
+        import torch
+
+        src = torch.ones(args.copy_probe << 18, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": src.numel() * 4, "launches": 4}), flush=True)
+        return
+
     from bramha_amd.plane import HipComputePlane
 
     plane = HipComputePlane(0)
+    if args.profile_eager:
+        m1, _ = build_model(plane, 1, args.prompt, 64)
+        t = m1.time_kernels(8)
+        print(json.dumps({k: v[0] for k, v in t.items()}), flush=True)
+        m1.close()
+        plane.close()
+        return
     if args.only_full:
         print(json.dumps({"ragged32": ragged_decode(plane), "qwen2_7b": qwen7b(plane)}), flush=True)
         plane.close()
@@ -333,7 +373,7 @@ def main():
     dt1 = timed_decode(m1, args.steps, args.warmup)
     tok1 = args.steps / dt1
     log("bs1: %.1f tok/s (%.3f ms/step)" % (tok1, dt1 * 1e3 / args.steps))
-    kern, roof = roofline(m1)
+    kern, roof = roofline(m1, traffic=True)
     log("dominant kernel %s: %.1f GB/s (%.1f%% of HBM peak)" % (kern, roof["achieved"], 100 * roof["frac"]))
     m1.close()
     bs32 = None
