@@ -135,8 +135,9 @@ def gemv_sweep(plane, rotate=1 << 30, iters=64):
 
 def attn_sweep(plane, rotate=1 << 30, iters=32, seed=0, nq=14, nkv=2, hd=64, contexts=(512, 4096, 32768),
                batches=(1, 8)):
-    """GQA decode attention alone: 14 query heads over 2 KV heads of 64, fp16 K/V N(0, 1) (V
-    stored transposed), one query token per sequence at the end of its context, softmax in f32.
+    """GQA decode attention alone: 14 query heads over 2 KV heads of 64, fp16 K/V N(0, 1) in the
+    decoder's MFMA-tile layout, one query token per sequence at the end of its context, softmax
+    in f32.
     Bytes = K + V rows read + queries + outputs."""
     import numpy as np
 
@@ -148,7 +149,8 @@ def attn_sweep(plane, rotate=1 << 30, iters=32, seed=0, nq=14, nkv=2, hd=64, con
         for B in batches:
             rows = T * B
             k = rng.standard_normal((nkv, rows, hd), dtype=np.float32).astype(np.float16)
-            v = rng.standard_normal((nkv, hd, rows), dtype=np.float32).astype(np.float16)
+            v = rng.standard_normal((nkv, rows, hd), dtype=np.float32).astype(np.float16)
+            k, v = ops.pack_kv_f16(k, v)  # the decoder's fp16 cache layout
             q = rng.standard_normal((B, nq * hd), dtype=np.float32)
             dk, dv, dq = (ops.DeviceArray.from_numpy(plane, a) for a in (k, v, q))
             off = ops.DeviceArray.from_numpy(plane, np.arange(B, dtype=np.int64) * T)

@@ -583,11 +583,14 @@ static int attn_args(bh_ctx* ctx, const float* q, const void* k, const void* v, 
     return BH_OK;
 }
 
-static int attn_check(bh_ctx* ctx, const float* q, const void* k, const void* v, const int64_t* seq_off,
-                      const int32_t* seq_len, float* out, int batch, int n_q, int n_kv, int head_dim, int max_len) {
+static int attn_check(bh_ctx* ctx, const float* q, const void* k, const void* v, int kv_f16, int64_t kv_rows,
+                      const int64_t* seq_off, const int32_t* seq_len, float* out, int batch, int n_q, int n_kv,
+                      int head_dim, int max_len) {
     if (!ctx || !q || !k || !v || !seq_off || !seq_len || !out || batch < 0 || n_q <= 0 || n_kv <= 0 ||
-        n_q % n_kv || max_len < 0)
+        n_q % n_kv || max_len < 0 || kv_rows <= 0)
         return BH_ERR_INVALID;
+    if (kv_f16 && kv_rows % 64)
+        return ctx->fail(BH_ERR_INVALID, "an fp16 KV cache holds whole 64-row tiles: kv_rows must be a multiple of 64");
     if (!attn_supported(n_q, n_kv, head_dim))
         return ctx->fail(BH_ERR_UNSUPPORTED, "attention supports head_dim 64/128 and 1, 2, 4, 7 or 8 query heads per KV head");
     return BH_OK;
@@ -596,7 +599,7 @@ static int attn_check(bh_ctx* ctx, const float* q, const void* k, const void* v,
 int bh_attn_decode(bh_ctx* ctx, const float* q, const void* k, const void* v, int kv_f16, int64_t kv_rows,
                    const int64_t* seq_off, const int32_t* seq_len, int batch, int n_q, int n_kv, int head_dim,
                    int max_len, float* out, void* stream) {
-    int rc = attn_check(ctx, q, k, v, seq_off, seq_len, out, batch, n_q, n_kv, head_dim, max_len);
+    int rc = attn_check(ctx, q, k, v, kv_f16, kv_rows, seq_off, seq_len, out, batch, n_q, n_kv, head_dim, max_len);
     if (rc) return rc;
     if (batch == 0) return BH_OK;
     std::lock_guard<std::mutex> g(ctx->mu);
@@ -692,7 +695,7 @@ int bh_time_gemv(bh_ctx* ctx, const bh_weight* wh, const float* x, float* y, int
 int bh_time_attn(bh_ctx* ctx, const float* q, const void* k, const void* v, int kv_f16, int64_t kv_rows,
                  const int64_t* seq_off, const int32_t* seq_len, int batch, int n_q, int n_kv, int head_dim,
                  int max_len, float* out, int iters, size_t rotate_bytes, double* us_per_launch) {
-    int rc = attn_check(ctx, q, k, v, seq_off, seq_len, out, batch, n_q, n_kv, head_dim, max_len);
+    int rc = attn_check(ctx, q, k, v, kv_f16, kv_rows, seq_off, seq_len, out, batch, n_q, n_kv, head_dim, max_len);
     if (rc) return rc;
     if (batch <= 0 || iters <= 0 || !us_per_launch) return BH_ERR_INVALID;
     std::lock_guard<std::mutex> g(ctx->mu);

@@ -55,9 +55,32 @@ enum Epi : int {
     EPI_LMHEAD = 4,   // logits -> y, repetition penalty, per-64-row argmax -> partial
 };
 
-// Packed KV cache of one layer. K is [n_kv][kv_rows][hd]. V is [n_kv][kv_rows][hd] in f32 and
-// transposed, [n_kv][hd][kv_rows], in fp16: the fp16 cache is read by the MFMA attention kernel,
-// whose V operand takes 8 consecutive rows of one column per lane.
+// Packed KV cache of one layer, one region of kv_rows rows per KV head (K and V alike).
+// f32 cache: row-major, element (t, d) of head h at (h * kv_rows + t) * hd + d.
+// fp16 cache: "MFMA tiles" — rows grouped in tiles of KV_TILE(hd) rows (64 at hd 64, 32 at
+// hd 128: 8 KiB each), and inside a tile the elements stored in the order the attention
+// kernel's wavefronts load their v_mfma_f32_16x16x32_f16 operands, so every operand load of a
+// wavefront is 1 KiB of contiguous bytes (64 lanes x 16 B). kv_k_off / kv_v_off give the
+// offset (in elements, from the head's base h * kv_rows * hd) of element (t, d).
+__host__ __device__ constexpr int KV_TILE(int hd) { return hd == 64 ? 64 : 32; }
+// K operand (16-row block blk, 32-wide chunk kc of the head dim) of lane (lr, lg) holds row
+// 32(blk/2) + 8(lr/4) + 4(blk%2) + lr%4 of the tile, dims 32kc + 8lg .. +7.
+__host__ __device__ inline int64_t kv_k_off(int64_t t, int d, int hd) {
+    const int tr = KV_TILE(hd), kcs = hd / 32;
+    const int r = (int)(t % tr);
+    const int blk = 2 * (r / 32) + (r % 8) / 4, lr = 4 * ((r % 32) / 8) + (r % 4);
+    const int kc = d / 32, lg = (d % 32) / 8;
+    return (t / tr) * (int64_t)tr * hd + ((int64_t)((blk * kcs + kc) * 64 + lr + 16 * lg) * 8 + d % 8);
+}
+// V^T operand (32-row group j, 16-wide dim block db) of lane (lr, lg) holds dim 16db + lr of
+// rows 32j + 8lg .. +7 of the tile.
+__host__ __device__ inline int64_t kv_v_off(int64_t t, int d, int hd) {
+    const int tr = KV_TILE(hd), dbs = hd / 16;
+    const int r = (int)(t % tr);
+    const int j = r / 32, lg = (r % 32) / 8;
+    const int db = d / 16, lr = d % 16;
+    return (t / tr) * (int64_t)tr * hd + ((int64_t)((j * dbs + db) * 64 + lr + 16 * lg) * 8 + r % 8);
+}
 struct KvView {
     void* k = nullptr;
     void* v = nullptr;

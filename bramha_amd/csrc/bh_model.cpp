@@ -79,6 +79,7 @@ struct bh_model {
     uint16_t* d_pen = nullptr;
     const float2* rope = nullptr;
     int max_pos = 0;
+    int kv_align = 8;  // rows: every sequence region starts on a multiple
     void* h_stage = nullptr;  // pinned staging for small host->device copies
 
     std::vector<int64_t> off_h, cap_h;
@@ -408,7 +409,10 @@ int bh_model_create(bh_ctx* ctx, const bh_model_config* cfg, bh_model** out) {
     bh_model* m = new bh_model();
     m->ctx = ctx;
     m->c = c;
-    m->c.kv_rows = (c.kv_rows + 7) / 8 * 8;  // sequence regions start on 8-row boundaries
+    // Sequence regions start on KV_ALIGN-row boundaries (fp16: whole MFMA tiles, f32: 16-byte
+    // loads); room for every slot's rounding is added so that capacities summing to kv_rows fit.
+    m->kv_align = c.kv_f16 ? 64 : 8;
+    m->c.kv_rows = (c.kv_rows + m->kv_align - 1) / m->kv_align * m->kv_align + (int64_t)m->kv_align * c.max_seqs;
     m->QD = QD;
     m->KD = KD;
     m->NQKV = QD + 2 * KD;
@@ -590,7 +594,7 @@ int bh_model_seq_open(bh_model* m, int slot, int64_t capacity) {
     if (slot < 0 || slot >= m->c.max_seqs) return m->fail(BH_ERR_INVALID, "slot out of range");
     if (m->c.max_context > 0) capacity = m->c.max_context;
     if (capacity <= 0) return m->fail(BH_ERR_INVALID, "capacity must be positive");
-    capacity = (capacity + 7) / 8 * 8;  // keeps every region 8-row aligned (16-byte V^T loads)
+    capacity = (capacity + m->kv_align - 1) / m->kv_align * m->kv_align;  // keeps regions aligned
     for (int b = 0; b < m->B; ++b)
         if (m->bslots[b] == slot) return m->fail(BH_ERR_INVALID, "slot is in the decode batch; replace it first");
     if (m->off_h[slot] < 0 || m->cap_h[slot] < capacity) {

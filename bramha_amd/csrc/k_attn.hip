@@ -340,39 +340,67 @@ struct AttnWave {
     static constexpr int NJ = KvTile<HD>::NJ;
     static constexpr int NB = 2 * NJ;   // 16-row MFMA blocks per tile
     static constexpr int TR = 32 * NJ;  // rows per tile
-    const __half* Kc;
-    const __half* Vt;
-    int64_t kv_rows;
-    bool v_aligned;
+    const __half* Kh;  // this KV head's K region (MFMA-tile order, kv_k_off)
+    const __half* Vh;  // this KV head's V region (kv_v_off)
+    int64_t off;       // the sequence's first row in the region
+    bool tiled;        // off is a multiple of 64 (tile-aligned) and kv_rows of 8: 1 KiB operand loads
+    bool v8;           // off and kv_rows are multiples of 8: 16-byte V loads
     int r0, r1, lim;
+    int lim_all;  // the smallest column limit of the wave (wave-uniform): tiles below it need no mask
     KvTile<HD> A, B;
 
     __device__ __forceinline__ void load_tile(KvTile<HD>& T, int t0) const {
         const int lane = threadIdx.x & 63;
         const int lr = lane & 15, lg = lane >> 4;
+        const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+        const bool part = t0 + TR > r1;  // wave-uniform: rows past r1 are not loaded (stale bytes)
+        if (tiled) {
+            const __half* kb = Kh + (off + t0) * HD;  // the tile's first element
+            const __half* vb = Vh + (off + t0) * HD;
+#pragma unroll
+            for (int blk = 0; blk < NB; ++blk) {
+                const bool ok = !part || t0 + mf_row(blk, lr) < r1;
+#pragma unroll
+                for (int kc = 0; kc < KC; ++kc)
+                    T.k[blk][kc] = ok ? *(const half8*)(kb + ((blk * KC + kc) * 64 + lane) * 8) : zero;
+            }
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                const int tg = t0 + 32 * j + 8 * lg;  // this lane group's 8 rows
+#pragma unroll
+                for (int db = 0; db < DB; ++db) {
+                    half8 v = (!part || tg < r1) ? *(const half8*)(vb + ((j * DB + db) * 64 + lane) * 8) : zero;
+                    if (part) {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) v[e] = tg + e < r1 ? v[e] : (_Float16)0.f;
+                    }
+                    T.v[j][db] = v;
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int blk = 0; blk < NB; ++blk) {
             const int t = t0 + mf_row(blk, lr);
 #pragma unroll
-            for (int kc = 0; kc < KC; ++kc) {
-                if (t < r1) T.k[blk][kc] = *(const half8*)(Kc + (int64_t)t * HD + kc * 32 + 8 * lg);
-                else T.k[blk][kc] = half8{0, 0, 0, 0, 0, 0, 0, 0};
-            }
+            for (int kc = 0; kc < KC; ++kc)
+                T.k[blk][kc] = t < r1 ? *(const half8*)(Kh + kv_k_off(off + t, kc * 32 + 8 * lg, HD)) : zero;
         }
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-            const int tg = t0 + 32 * j + 8 * lg;  // this lane group's 8 rows
+            const int tg = t0 + 32 * j + 8 * lg;
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
-                const __half* p = Vt + (int64_t)(db * 16 + lr) * kv_rows + tg;
-                if (v_aligned && tg + 7 < r1) {
-                    T.v[j][db] = *(const half8*)p;
+                half8 v;
+                if (v8 && tg + 7 < r1) {
+                    v = *(const half8*)(Vh + kv_v_off(off + tg, db * 16 + lr, HD));
                 } else {
-                    half8 v;
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) v[e] = tg + e < r1 ? (_Float16)__half2float(p[e]) : (_Float16)0.f;
-                    T.v[j][db] = v;
+                    for (int e = 0; e < 8; ++e)
+                        v[e] = tg + e < r1 ? (_Float16)__half2float(Vh[kv_v_off(off + tg + e, db * 16 + lr, HD)])
+                                           : (_Float16)0.f;
                 }
+                T.v[j][db] = v;
             }
         }
     }
@@ -382,12 +410,13 @@ struct AttnWave {
         if (t < r1) load_tile(A, t);
     }
 
-    __device__ __forceinline__ void compute(const KvTile<HD>& T, int t0, const half8 (&qh)[KC], const half8 (&ql)[KC],
-                                            float& m, float& l, f32x4 (&o)[DB]) const {
+    // MASK: some row of the tile is at or past a column's limit (the tile straddles lim).
+    template <bool MASK>
+    __device__ __forceinline__ void compute_t(const KvTile<HD>& T, int t0, const half8 (&qh)[KC],
+                                              const half8 (&ql)[KC], float& m, float& l, f32x4 (&o)[DB]) const {
         const int lane = threadIdx.x & 63;
         const int lg = lane >> 4;
-        const float scale2 = 1.4426950408889634f / sqrtf((float)HD);
-        // S^T: lane holds rows mf_row(blk, 4lg + v) of column lr
+        // S^T (queries pre-scaled by log2(e)/sqrt(hd)): lane holds rows mf_row(blk, 4lg + v) of column lr
         f32x4 sc[NB];
 #pragma unroll
         for (int blk = 0; blk < NB; ++blk) {
@@ -404,48 +433,49 @@ struct AttnWave {
         for (int blk = 0; blk < NB; ++blk)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const bool ok = t0 + mf_row(blk, 4 * lg + v) < lim;
-                sc[blk][v] = ok ? sc[blk][v] * scale2 : -INFINITY;
+                if constexpr (MASK) sc[blk][v] = t0 + mf_row(blk, 4 * lg + v) < lim ? sc[blk][v] : -INFINITY;
                 tmax = fmaxf(tmax, sc[blk][v]);
             }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
         const float mn = fmaxf(m, tmax);  // without MASKCOL finite: row t0 of the tile is valid
-        float alpha = exp2f(m - mn);      // 0 while m is -inf
+        float alpha = __builtin_amdgcn_exp2f(m - mn);  // 0 while m is -inf
         if constexpr (MASKCOL) alpha = mn == -INFINITY ? 1.f : alpha;
         m = mn;
+        // P as fp16 hi + lo (hi + lo carries ~22 bits of the f32 probability)
+        half8 ph[NJ], pl[NJ];
         float ps = 0.f;
-        float pr[NB][4];
 #pragma unroll
-        for (int blk = 0; blk < NB; ++blk)
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                float p = exp2f(sc[blk][v] - mn);  // 0 for masked rows
-                if constexpr (MASKCOL) p = sc[blk][v] == -INFINITY ? 0.f : p;
-                pr[blk][v] = p;
+            for (int s = 0; s < 8; ++s) {
+                // slots s = 0..3 are block 2j, s = 4..7 block 2j+1: rows 32j + 8lg + s, the rows
+                // of the lane's V^T operand
+                const float x = sc[2 * j + (s >> 2)][s & 3];
+                float p = __builtin_amdgcn_exp2f(x - mn);  // 0 for masked rows
+                if constexpr (MASKCOL) p = x == -INFINITY ? 0.f : p;
+                const _Float16 h = (_Float16)p;
+                ph[j][s] = h;
+                pl[j][s] = (_Float16)(p - (float)h);
                 ps += p;
             }
         l = l * alpha + ps;
 #pragma unroll
         for (int db = 0; db < DB; ++db) o[db] *= alpha;
-        // O^T += V^T . P^T over rows 32j .. 32j+31: the lane's P slots s = 0..3 are block 2j,
-        // s = 4..7 block 2j+1 — rows 32j + 8lg + s, the rows of its V^T operand
+        // O^T += V^T . P^T over rows 32j .. 32j+31
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            float pv[8];
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                pv[v] = pr[2 * j][v];
-                pv[4 + v] = pr[2 * j + 1][v];
-            }
-            half8 ph, pl;
-            split_hl(pv, ph, pl);
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(T.v[j][db], ph, o[db], 0, 0, 0);
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(T.v[j][db], pl, o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(T.v[j][db], ph[j], o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(T.v[j][db], pl[j], o[db], 0, 0, 0);
             }
-        }
+    }
+
+    __device__ __forceinline__ void compute(const KvTile<HD>& T, int t0, const half8 (&qh)[KC], const half8 (&ql)[KC],
+                                            float& m, float& l, f32x4 (&o)[DB]) const {
+        if (t0 + TR <= lim_all) compute_t<false>(T, t0, qh, ql, m, l, o);  // wave-uniform
+        else compute_t<true>(T, t0, qh, ql, m, l, o);
     }
 
     __device__ __forceinline__ void run(const half8 (&qh)[KC], const half8 (&ql)[KC], float& m, float& l, f32x4 (&o)[DB]) {
@@ -501,9 +531,10 @@ __global__ void __launch_bounds__(64 * NW) k_attn_mf(const AttnArgs a) {
     }
     const int r0 = sp * a.split_rows;
     const int r1 = min(len, r0 + a.split_rows);
-    const __half* Kc = (const __half*)a.kv.k + ((int64_t)h * a.kv.kv_rows + off) * HD;
-    const __half* Vt = (const __half*)a.kv.v + (int64_t)h * HD * a.kv.kv_rows + off;  // + d * kv_rows + t
-    AttnWave<HD, NW, false> aw{Kc, Vt, a.kv.kv_rows, ((off | a.kv.kv_rows) & 7) == 0, r0, r1, r1};
+    const int64_t head = (int64_t)h * a.kv.kv_rows * HD;
+    AttnWave<HD, NW, false> aw{(const __half*)a.kv.k + head, (const __half*)a.kv.v + head, off,
+                               (off & 63) == 0 && (a.kv.kv_rows & 7) == 0, ((off | a.kv.kv_rows) & 7) == 0,
+                               r0, r1, r1, r1};
     aw.start();
 
     // q rows into LDS, then Q^T as the B operand:
@@ -511,7 +542,7 @@ __global__ void __launch_bounds__(64 * NW) k_attn_mf(const AttnArgs a) {
 #pragma unroll
     for (int k = 0; k < QPT; ++k) {
         const int i = threadIdx.x + k * NT;
-        q_s[i / HD][i % HD] = qreg[k];
+        q_s[i / HD][i % HD] = qreg[k] * (1.4426950408889634f / sqrtf((float)HD));
     }
     __syncthreads();
     half8 qh[KC], ql[KC];
@@ -666,15 +697,19 @@ __global__ void __launch_bounds__(64 * NW) k_attn_pf(const AttnArgs a) {
     int r1 = lim;
 #pragma unroll
     for (int sh = 8; sh > 0; sh >>= 1) r1 = max(r1, __shfl_xor(r1, sh));
-    const __half* Kc = (const __half*)a.kv.k + ((int64_t)h * a.kv.kv_rows + off) * HD;
-    const __half* Vt = (const __half*)a.kv.v + (int64_t)h * HD * a.kv.kv_rows + off;
-    AttnWave<HD, NW, true> aw{Kc, Vt, a.kv.kv_rows, ((off | a.kv.kv_rows) & 7) == 0, 0, r1, lim};
+    const int64_t head = (int64_t)h * a.kv.kv_rows * HD;
+    int lim_all = lr < ntok ? lim : 0x7fffffff;  // columns past the chunk never bind
+#pragma unroll
+    for (int sh = 8; sh > 0; sh >>= 1) lim_all = min(lim_all, __shfl_xor(lim_all, sh));
+    AttnWave<HD, NW, true> aw{(const __half*)a.kv.k + head, (const __half*)a.kv.v + head, off,
+                              (off & 63) == 0 && (a.kv.kv_rows & 7) == 0, ((off | a.kv.kv_rows) & 7) == 0,
+                              0, r1, lim, __builtin_amdgcn_readfirstlane(lim_all)};
     aw.start();
 
 #pragma unroll
     for (int k = 0; k < QPT; ++k) {
         const int i = threadIdx.x + k * NT;
-        q_s[i / HD][i % HD] = qreg[k];
+        q_s[i / HD][i % HD] = qreg[k] * (1.4426950408889634f / sqrtf((float)HD));
     }
     __syncthreads();
     half8 qh[KC], ql[KC];

@@ -162,13 +162,12 @@ __device__ __forceinline__ void run_epilogue(const GemvArgs& a, const float* fin
                 a.y[(int64_t)b * a.ldy + nn] = val;
             } else {
                 const int64_t row = a.boff[b] + kv_phys_row(a.kv, p);
-                if (sec == 2 && a.kv.kv_f16) {  // fp16 V is stored transposed
-                    ((__half*)a.kv.v)[((int64_t)hh * a.hd + d) * a.kv.kv_rows + row] = __float2half(val);
+                const int64_t head = (int64_t)hh * a.kv.kv_rows * a.hd;
+                if (a.kv.kv_f16) {  // MFMA-tile order (kv_k_off / kv_v_off)
+                    if (sec == 1) ((__half*)a.kv.k)[head + kv_k_off(row, d, a.hd)] = __float2half(val);
+                    else ((__half*)a.kv.v)[head + kv_v_off(row, d, a.hd)] = __float2half(val);
                 } else {
-                    const int64_t off = ((int64_t)hh * a.kv.kv_rows + row) * a.hd + d;
-                    void* base = sec == 1 ? a.kv.k : a.kv.v;
-                    if (a.kv.kv_f16) ((__half*)base)[off] = __float2half(val);
-                    else ((float*)base)[off] = val;
+                    ((float*)(sec == 1 ? a.kv.k : a.kv.v))[head + row * a.hd + d] = val;
                 }
             }
         }

@@ -143,6 +143,18 @@ __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
             }
         };
         if (c0 < c1) fetch(c0, q0, s0);
+        // The activations reach the FMAs through scalar loads issued chunk by chunk; they were
+        // just written by the previous kernel (often on another XCD), so a first touch here, one
+        // vector load per 128-byte line of the workgroup's range, brings them into L2 while the
+        // first weight stage is in flight (bs1 decode step: 1232 -> 1291 tok/s). The value is
+        // consumed only after the main loop, so nothing waits on it early.
+        float touch = 0.f;
+        {
+            const int nx = (wc1 - wc0) * E;
+            for (int bb = 0; bb < B; ++bb)
+                for (int i2 = threadIdx.x * 32; i2 < nx; i2 += blockDim.x * 32)
+                    touch += a.x[(int64_t)bb * a.ldx + wc0 * E + i2];
+        }
         load_rnorm<B>(a, rn);
 
         float acc[NACC][B];
@@ -191,6 +203,7 @@ __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
         for (int j = 0; j < NACC; ++j)
 #pragma unroll
             for (int b = 0; b < B; ++b) comb[kw * TOT + (j * B + b) * ROWS + r] = acc[j][b];
+        asm volatile("" ::"v"(touch));
     }
 
     // ---- combine the K-split partial sums in a fixed order ----

@@ -115,12 +115,40 @@ def silu_mul(plane, g, u):
     return out
 
 
+def kv_tile_index(rows, hd):
+    """Element offsets (within one head's region) of the fp16 cache's MFMA-tile layout for a
+    [rows][hd] block: (k_idx, v_idx), each [rows][hd] int64 (bh_attn_decode's kv_k_off /
+    kv_v_off). rows must be a multiple of 64."""
+    tr = 64 if hd == 64 else 32
+    t = np.arange(rows, dtype=np.int64)[:, None]
+    d = np.arange(hd, dtype=np.int64)[None, :]
+    r, base = t % tr, (t // tr) * tr * hd
+    blk, lr = 2 * (r // 32) + (r % 8) // 4, 4 * ((r % 32) // 8) + r % 4
+    k_idx = base + ((blk * (hd // 32) + d // 32) * 64 + lr + 16 * ((d % 32) // 8)) * 8 + d % 8
+    v_idx = base + (((r // 32) * (hd // 16) + d // 16) * 64 + d % 16 + 16 * ((r % 32) // 8)) * 8 + r % 8
+    return k_idx, v_idx
+
+
+def pack_kv_f16(k, v):
+    """Row-major K, V [n_kv, rows, hd] (rows a multiple of 64) -> the fp16 cache layout of
+    bh_attn_decode, two fp16 arrays [n_kv, rows * hd]."""
+    nkv, rows, hd = k.shape
+    ki, vi = kv_tile_index(rows, hd)
+    kp = np.empty((nkv, rows * hd), np.float16)
+    vp = np.empty((nkv, rows * hd), np.float16)
+    for h in range(nkv):
+        kp[h, ki.ravel()] = k[h].astype(np.float16).ravel()
+        vp[h, vi.ravel()] = v[h].astype(np.float16).ravel()
+    return kp, vp
+
+
 def attn_decode(plane, q, k, v, seq_off, seq_len, n_q, n_kv, head_dim, max_len):
-    """q: [B, n_q*hd] f32; k: [n_kv, rows, hd]; v: [n_kv, rows, hd] in f32 or [n_kv, hd, rows] in
-    f16; seq_off int64 [B]; seq_len int32 [B] (all DeviceArrays)."""
+    """q: [B, n_q*hd] f32; k, v: [n_kv, rows, hd] row-major f32, or [n_kv, rows*hd] fp16 in the
+    tile layout (pack_kv_f16); seq_off int64 [B]; seq_len int32 [B] (all DeviceArrays)."""
     out = DeviceArray(plane, q.shape, np.float32)
     kv_f16 = 1 if k.dtype == np.float16 else 0
-    check(lib.bh_attn_decode(plane.ctx, q.ptr, k.ptr, v.ptr, kv_f16, k.shape[1], seq_off.ptr, seq_len.ptr,
+    rows = k.shape[1] // head_dim if kv_f16 else k.shape[1]
+    check(lib.bh_attn_decode(plane.ctx, q.ptr, k.ptr, v.ptr, kv_f16, rows, seq_off.ptr, seq_len.ptr,
                              q.shape[0], n_q, n_kv, head_dim, max_len, out.ptr, None), plane.ctx)
     return out
 
@@ -130,8 +158,9 @@ def time_attn(plane, q, k, v, seq_off, seq_len, n_q, n_kv, head_dim, max_len, it
     copies totalling rotate_bytes."""
     out = DeviceArray(plane, q.shape, np.float32)
     kv_f16 = 1 if k.dtype == np.float16 else 0
+    rows = k.shape[1] // head_dim if kv_f16 else k.shape[1]
     us = ctypes.c_double()
-    check(lib.bh_time_attn(plane.ctx, q.ptr, k.ptr, v.ptr, kv_f16, k.shape[1], seq_off.ptr, seq_len.ptr,
+    check(lib.bh_time_attn(plane.ctx, q.ptr, k.ptr, v.ptr, kv_f16, rows, seq_off.ptr, seq_len.ptr,
                            q.shape[0], n_q, n_kv, head_dim, max_len, out.ptr, iters, rotate_bytes,
                            ctypes.byref(us)), plane.ctx)
     out.free()

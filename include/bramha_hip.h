@@ -132,13 +132,22 @@ int bh_rope(bh_ctx* ctx, float* v, const int32_t* pos, int rows, int n_heads, in
 /* out = g * (1 / (1 + exp(-g))) * u   (cpu_engine.rs:2023-2026) */
 int bh_silu_mul(bh_ctx* ctx, const float* g, const float* u, float* out, int64_t n, void* stream);
 /* GQA decode attention for `batch` query rows (flash_attention_single_into,
- * cpu_engine.rs:1450-1509). q: f32 [batch][n_q*head_dim]. The packed cache: K is head-major
- * [n_kv][kv_rows][head_dim]; V is [n_kv][kv_rows][head_dim] in f32 (kv_f16 = 0) and transposed,
- * [n_kv][head_dim][kv_rows], in fp16 (kv_f16 = 1) — the layout the device decoder keeps.
+ * cpu_engine.rs:1450-1509). q: f32 [batch][n_q*head_dim]. The packed cache has one region of
+ * kv_rows rows per KV head for K and for V, in the layout the device decoder keeps:
+ *  - f32 (kv_f16 = 0): row-major, element (row t, dim d) of head h at (h*kv_rows + t)*head_dim + d;
+ *  - fp16 (kv_f16 = 1): "MFMA tiles" of 64 rows (head_dim 64) or 32 rows (head_dim 128), each
+ *    stored in the order the attention kernel loads its matrix-core operands; element (t, d) of
+ *    head h is at h*kv_rows*head_dim + kv_k_off(t, d) for K and + kv_v_off(t, d) for V, where
+ *    with TR the tile rows, r = t % TR, base = (t / TR)*TR*head_dim:
+ *      kv_k_off = base + ((blk*(head_dim/32) + d/32)*64 + lr + 16*((d%32)/8))*8 + d%8,
+ *        blk = 2*(r/32) + (r%8)/4, lr = 4*((r%32)/8) + r%4;
+ *      kv_v_off = base + (((r/32)*(head_dim/16) + d/16)*64 + d%16 + 16*((r%32)/8))*8 + r%8;
+ *    kv_rows must be a multiple of 64.
  * Row b attends to cache rows [seq_off[b], seq_off[b] + seq_len[b]) (device int64 / int32
- * arrays; the offsets are prefix sums of the sequences' capacities; offsets and kv_rows that
- * are multiples of 8 take the 16-byte load path). max_len bounds seq_len and sizes the split
- * over the context. out: f32 [batch][n_q*head_dim]. */
+ * arrays; the offsets are prefix sums of the sequences' capacities). fp16 offsets that are
+ * multiples of 64 take the 1 KiB operand loads, multiples of 8 16-byte loads; f32 offsets and
+ * kv_rows that are multiples of 8 take 16-byte loads. max_len bounds seq_len and sizes the
+ * split over the context. out: f32 [batch][n_q*head_dim]. */
 int bh_attn_decode(bh_ctx* ctx, const float* q, const void* k, const void* v, int kv_f16, int64_t kv_rows,
                    const int64_t* seq_off, const int32_t* seq_len, int batch, int n_q, int n_kv, int head_dim,
                    int max_len, float* out, void* stream);

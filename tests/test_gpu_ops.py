@@ -185,19 +185,31 @@ def test_rmsnorm_rope_silu(plane):
     assert np.max(np.abs(got - want)) < 2e-6 * np.abs(want).max()
 
 
-def _attn_case(plane, lens, nq=14, nkv=2, hd=64, kv_f16=True, seed=0, check_rows=None):
+def _attn_case(plane, lens, nq=14, nkv=2, hd=64, kv_f16=True, seed=0, check_rows=None, align=1):
+    """Sequences at prefix-sum offsets (each capacity rounded up to `align` rows); every cache row
+    outside the sequences is NaN, so a kernel that lets a stale row into a sum fails."""
     D = lambda a: ops.DeviceArray.from_numpy(plane, a)  # noqa: E731
     rng = np.random.default_rng(seed)
     B = len(lens)
-    offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)  # prefix sums
-    rows = int(np.sum(lens))
-    kdt = np.float16 if kv_f16 else np.float32
-    k = rng.standard_normal((nkv, rows, hd)).astype(kdt)
-    v = rng.standard_normal((nkv, rows, hd)).astype(kdt)
+    caps = [(n + align - 1) // align * align for n in lens]
+    offs = np.concatenate([[0], np.cumsum(caps)[:-1]]).astype(np.int64)  # prefix sums
+    rows = int(np.sum(caps))
+    if kv_f16:
+        rows = (rows + 63) // 64 * 64  # whole tiles
+    k = np.full((nkv, rows, hd), np.nan, np.float32)
+    v = np.full((nkv, rows, hd), np.nan, np.float32)
+    for b in range(B):
+        k[:, offs[b]:offs[b] + lens[b]] = rng.standard_normal((nkv, lens[b], hd))
+        v[:, offs[b]:offs[b] + lens[b]] = rng.standard_normal((nkv, lens[b], hd))
+    if kv_f16:
+        k, v = k.astype(np.float16), v.astype(np.float16)
+        kdev, vdev = ops.pack_kv_f16(k, v)
+    else:
+        kdev, vdev = k, v
     q = rng.standard_normal((B, nq * hd)).astype(np.float32)
-    vdev = np.ascontiguousarray(v.transpose(0, 2, 1)) if kv_f16 else v  # fp16 V is stored [nkv][hd][rows]
-    out = ops.attn_decode(plane, D(q), D(k), D(vdev), D(offs), D(np.array(lens, np.int32)), nq, nkv, hd,
+    out = ops.attn_decode(plane, D(q), D(kdev), D(vdev), D(offs), D(np.array(lens, np.int32)), nq, nkv, hd,
                           int(max(lens))).numpy()
+    assert np.all(np.isfinite(out))
     for b in (check_rows if check_rows is not None else range(B)):
         kc = k[:, offs[b]:offs[b] + lens[b]].astype(np.float32).transpose(1, 0, 2)  # -> [T][nkv][hd]
         vc = v[:, offs[b]:offs[b] + lens[b]].astype(np.float32).transpose(1, 0, 2)
@@ -213,6 +225,9 @@ def test_attention_config3(plane, T, B):
 
 
 def test_attention_ragged_and_short(plane):
-    _attn_case(plane, [1, 2, 63, 64, 65, 200, 257, 1000], seed=1)
+    _attn_case(plane, [1, 2, 63, 64, 65, 200, 257, 1000], seed=1)  # unaligned offsets
+    _attn_case(plane, [1, 2, 63, 64, 65, 200, 257, 1000], seed=4, align=8)  # 8-row aligned
+    _attn_case(plane, [1, 2, 63, 64, 65, 200, 257, 1000], seed=5, align=64)  # whole tiles (decoder layout)
+    _attn_case(plane, [130, 7, 64], nq=28, nkv=4, hd=128, seed=6, align=64)
     _attn_case(plane, [5, 300], kv_f16=False, seed=2)
     _attn_case(plane, [130, 7], nq=28, nkv=4, hd=128, seed=3)  # Qwen2-7B heads

@@ -97,3 +97,22 @@ def test_cpu_only_mode_falls_back(monkeypatch):
     h = np.ones(896, np.float32)
     w = np.ones((896, 896), np.float32)
     assert try_gpu_matvec(h, "f32", w, None, 896) is None  # the caller runs its CPU GEMV
+
+
+def test_kv_tile_layout():
+    """The fp16 cache layout is a permutation of each head's region, and the first operand of a
+    tile — MFMA block 0 / chunk 0 for K, row group 0 / dim block 0 for V — is lane-ordered: lane
+    (lr, lg) = lane % 16, lane // 16 holds its 8 elements at offsets 8 lane .. 8 lane + 7."""
+    import numpy as np
+
+    from bramha_amd import ops
+
+    for hd in (64, 128):
+        ki, vi = ops.kv_tile_index(128, hd)
+        for idx in (ki, vi):
+            assert np.array_equal(np.sort(idx.ravel()), np.arange(128 * hd))
+        for lane in range(64):
+            lr, lg = lane % 16, lane // 16
+            row = 8 * (lr >> 2) + (lr & 3)  # row of block 0, lane-group row lr
+            assert list(ki[row, 8 * lg:8 * lg + 8]) == list(range(8 * lane, 8 * lane + 8))
+            assert list(vi[8 * lg:8 * lg + 8, lr]) == list(range(8 * lane, 8 * lane + 8))
