@@ -94,6 +94,10 @@ _PROTOS = {
     "bh_time_attn": (c_int, [_P, _P, _P, _P, c_int, c_int64, _P, _P, c_int, c_int, c_int, c_int, c_int, _P, c_int,
                              c_size_t, POINTER(c_double)]),
     "bh_model_create": (c_int, [_P, POINTER(bh_model_config), POINTER(c_void_p)]),
+    "bh_model_load_dir": (c_int, [_P, c_char_p, POINTER(c_int)]),
+    "bh_model_kv_read": (c_int, [_P, c_int, c_int64, c_int64, _P, _P]),
+    "bh_model_kv_write": (c_int, [_P, c_int, c_int64, c_int64, _P, _P]),
+    "bh_model_seq_len": (c_int, [_P, c_int, POINTER(c_int64)]),
     "bh_model_destroy": (None, [_P]),
     "bh_model_set_weight": (c_int, [_P, c_char_p, _P, c_size_t, _P, c_size_t]),
     "bh_model_missing": (c_int, [_P, POINTER(c_int)]),

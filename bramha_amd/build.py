@@ -22,6 +22,7 @@ SOURCES = [
     "csrc/bh_host.cpp",
     "csrc/bh_api.cpp",
     "csrc/bh_model.cpp",
+    "csrc/bh_loader.cpp",
 ]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

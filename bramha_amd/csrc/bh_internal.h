@@ -193,6 +193,10 @@ hipError_t launch_rmsnorm(const float* x, const float* w, float eps, float* out,
 hipError_t launch_rope(float* v, const int32_t* pos, const float2* tab, int rows, int n_heads, int hd, hipStream_t st);
 hipError_t launch_silu_mul(const float* g, const float* u, float* out, int64_t n, hipStream_t st);
 hipError_t launch_dequant(const DevWeight& w, float* out, hipStream_t st);
+// Rows [row0, row0 + n) (absolute rows of the packed buffer) of one layer's cache <-> f32
+// [n][nkv][hd] (to_host = 1: cache -> kh / vh; 0: kh / vh -> cache).
+hipError_t launch_kv_copy(const KvView& kv, int nkv, int hd, int64_t row0, int64_t n, float* kh, float* vh, int to_host,
+                          hipStream_t st);
 // Start of the residual stream for `batch` tokens tok[b] % vocab: x = embedding row of the tied
 // table (KM16, F32 or Q4_G32), xw = x * w0, ssq per 64 elements. reset_step != null: zero it.
 hipError_t launch_embed(const DevWeight& table, const int32_t* tok, const float* w0, float* x, float* xw, float* ssq,

@@ -574,6 +574,20 @@ int bh_model_set_weight(bh_model* m, const char* name, const void* data, size_t 
     return rc;
 }
 
+const char* model_last_error(bh_model* m) { return m->ctx->err.c_str(); }
+int model_load_dir(bh_model* m, const char* dir, int* n_loaded, std::string* err);  // bh_loader.cpp
+
+int bh_model_load_dir(bh_model* m, const char* dir, int* n_loaded) {
+    if (!m || !dir || !n_loaded) return BH_ERR_INVALID;
+    std::string err;
+    const int rc = model_load_dir(m, dir, n_loaded, &err);
+    if (rc != BH_OK) {
+        std::lock_guard<std::mutex> g(m->ctx->mu);
+        return m->fail(rc, err);
+    }
+    return BH_OK;
+}
+
 int bh_model_missing(bh_model* m, int* n_missing) {
     if (!m || !n_missing) return BH_ERR_INVALID;
     int miss = (m->have_embed ? 0 : 1) + (m->have_norm ? 0 : 1);
@@ -611,6 +625,63 @@ int bh_model_seq_open(bh_model* m, int slot, int64_t capacity) {
     hipError_t e = hipMemsetAsync(m->d_pen + (size_t)slot * m->c.vocab, 0, (size_t)m->c.vocab * 2, m->st);
     if (e == hipSuccess) e = hipStreamSynchronize(m->st);
     return e == hipSuccess ? BH_OK : m->ctx->hip_fail(e, "seq_open");
+}
+
+// KV rows of a slot <-> the reference's per-layer host layout (LayerKvCache, cpu_engine.rs:
+// 1720-1755; the flat vectors prefix_cache.rs:11-12 stores): k/v [layer][n][n_kv * head_dim] f32.
+static int kv_rows_io(bh_model* m, int slot, int64_t row0, int64_t n, float* k, float* v, int to_host) {
+    const bh_model_config& c = m->c;
+    if (slot < 0 || slot >= c.max_seqs || !m->open_h[slot]) return m->fail(BH_ERR_INVALID, "slot is not open");
+    if (row0 < 0 || n < 0 || row0 + n > m->cap_h[slot]) return m->fail(BH_ERR_CAPACITY, "rows outside the slot's KV region");
+    if (c.max_context > 0 && row0 + n > c.max_context)
+        return m->fail(BH_ERR_UNSUPPORTED, "KV rows past max_context are ring slots, not positions");
+    if (n == 0) return BH_OK;
+    const size_t per = (size_t)n * m->KD, bytes = per * 4;
+    float* dk = nullptr;
+    hipError_t e = hipMalloc(&dk, 2 * bytes);
+    float* dv = dk + per;
+    for (int l = 0; l < c.n_layers && e == hipSuccess; ++l) {
+        if (!to_host) {
+            e = hipMemcpyAsync(dk, k + (size_t)l * per, bytes, hipMemcpyHostToDevice, m->st);
+            if (e == hipSuccess) e = hipMemcpyAsync(dv, v + (size_t)l * per, bytes, hipMemcpyHostToDevice, m->st);
+        }
+        if (e == hipSuccess)
+            e = launch_kv_copy(kv_view(m, l), c.n_kv_heads, c.head_dim, m->off_h[slot] + row0, n, dk, dv, to_host, m->st);
+        if (e == hipSuccess && to_host) {
+            e = hipMemcpyAsync(k + (size_t)l * per, dk, bytes, hipMemcpyDeviceToHost, m->st);
+            if (e == hipSuccess) e = hipMemcpyAsync(v + (size_t)l * per, dv, bytes, hipMemcpyDeviceToHost, m->st);
+        }
+        if (e == hipSuccess) e = hipStreamSynchronize(m->st);  // the staging buffer is reused
+    }
+    if (dk) hipFree(dk);
+    return e == hipSuccess ? BH_OK : m->ctx->hip_fail(e, "KV rows copy");
+}
+
+int bh_model_kv_read(bh_model* m, int slot, int64_t row0, int64_t n, float* k_out, float* v_out) {
+    if (!m || (n > 0 && (!k_out || !v_out))) return BH_ERR_INVALID;
+    std::lock_guard<std::mutex> g(m->ctx->mu);
+    if (slot >= 0 && slot < m->c.max_seqs && row0 + n > m->len_h[slot])
+        return m->fail(BH_ERR_INVALID, "rows past the slot's length");
+    return kv_rows_io(m, slot, row0, n, k_out, v_out, 1);
+}
+
+int bh_model_kv_write(bh_model* m, int slot, int64_t row0, int64_t n, const float* k_in, const float* v_in) {
+    if (!m || (n > 0 && (!k_in || !v_in))) return BH_ERR_INVALID;
+    std::lock_guard<std::mutex> g(m->ctx->mu);
+    for (int b = 0; b < m->B; ++b)
+        if (m->bslots[b] == slot) return m->fail(BH_ERR_INVALID, "slot is in the decode batch; replace it first");
+    if (slot >= 0 && slot < m->c.max_seqs && row0 > m->len_h[slot])
+        return m->fail(BH_ERR_INVALID, "rows would leave a gap after the slot's length");
+    const int rc = kv_rows_io(m, slot, row0, n, (float*)k_in, (float*)v_in, 0);
+    if (rc == BH_OK) m->len_h[slot] = row0 + n;
+    return rc;
+}
+
+int bh_model_seq_len(bh_model* m, int slot, int64_t* len) {
+    if (!m || !len || slot < 0 || slot >= m->c.max_seqs) return BH_ERR_INVALID;
+    std::lock_guard<std::mutex> g(m->ctx->mu);
+    *len = m->open_h[slot] ? m->len_h[slot] : 0;
+    return BH_OK;
 }
 
 int bh_model_prefill(bh_model* m, int slot, const uint32_t* tokens, int n) {

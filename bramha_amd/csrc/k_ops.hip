@@ -183,6 +183,39 @@ __global__ void __launch_bounds__(256) k_sample(const SampleArgs a, const DevWei
     embed_stream(t, s_id, a.w0, a.x, a.xw, a.ssq, a.ssq_tiles, b);
 }
 
+// Cache rows <-> host-layout f32 rows (one thread per element, grid-stride).
+__global__ void __launch_bounds__(256) k_kv_copy(const KvView kv, int nkv, int hd, int64_t row0, int64_t n, float* kh,
+                                                 float* vh, int to_host) {
+    const int64_t total = n * nkv * hd;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / (nkv * hd);
+        const int rem = (int)(i % (nkv * hd));
+        const int h = rem / hd, d = rem % hd;
+        const int64_t row = row0 + r, head = (int64_t)h * kv.kv_rows * hd;
+        if (kv.kv_f16) {
+            __half* K = (__half*)kv.k + head + kv_k_off(row, d, hd);
+            __half* V = (__half*)kv.v + head + kv_v_off(row, d, hd);
+            if (to_host) {
+                kh[i] = __half2float(*K);
+                vh[i] = __half2float(*V);
+            } else {
+                *K = __float2half(kh[i]);
+                *V = __float2half(vh[i]);
+            }
+        } else {
+            float* K = (float*)kv.k + head + row * hd + d;
+            float* V = (float*)kv.v + head + row * hd + d;
+            if (to_host) {
+                kh[i] = *K;
+                vh[i] = *V;
+            } else {
+                *K = kh[i];
+                *V = vh[i];
+            }
+        }
+    }
+}
+
 }  // namespace
 
 hipError_t launch_rmsnorm(const float* x, const float* w, float eps, float* out, int rows, int n, hipStream_t st) {
@@ -198,6 +231,15 @@ hipError_t launch_rope(float* v, const int32_t* pos, const float2* tab, int rows
 hipError_t launch_silu_mul(const float* g, const float* u, float* out, int64_t n, hipStream_t st) {
     const int64_t blocks = std::min<int64_t>((n + 255) / 256, 4096);
     launch_kernel(k_silu_mul, dim3((unsigned)std::max<int64_t>(blocks, 1)), dim3(256), 0, st, g, u, out, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_copy(const KvView& kv, int nkv, int hd, int64_t row0, int64_t n, float* kh, float* vh, int to_host,
+                          hipStream_t st) {
+    const int64_t total = n * nkv * hd;
+    if (total <= 0) return hipSuccess;
+    const int64_t blocks = std::min<int64_t>((total + 255) / 256, 16384);
+    launch_kernel(k_kv_copy, dim3((unsigned)blocks), dim3(256), 0, st, kv, nkv, hd, row0, n, kh, vh, to_host);
     return hipGetLastError();
 }
 

@@ -5,6 +5,7 @@ Config fields mirror what generate_cpu_inner_logits reads from config.json
 KV element type, slots and KV rows).
 """
 import ctypes
+import os
 from dataclasses import asdict, dataclass
 
 import numpy as np
@@ -171,6 +172,34 @@ class HipDecoder:
         self._check(lib.bh_model_missing(self.m, ctypes.byref(n)))
         if n.value:
             raise ValueError("%d tensors missing" % n.value)
+
+    def load_dir(self, path):
+        """Load a model directory in the reference's on-disk format (bh_model_load_dir); returns
+        the number of tensors uploaded."""
+        n = ctypes.c_int()
+        self._check(lib.bh_model_load_dir(self.m, os.fsencode(path), ctypes.byref(n)))
+        return n.value
+
+    def kv_read(self, slot, row0, n):
+        """KV rows [row0, row0 + n) of a slot -> (k, v) f32 [n_layers, n, n_kv * head_dim]."""
+        c = self.cfg
+        k = np.empty((c.n_layers, n, c.kv_dim), np.float32)
+        v = np.empty_like(k)
+        self._check(lib.bh_model_kv_read(self.m, slot, row0, n, ptr(k), ptr(v)))
+        return k, v
+
+    def kv_write(self, slot, row0, k, v):
+        """Write KV rows starting at row0 (k, v f32 [n_layers, n, n_kv * head_dim]); the slot's
+        length becomes row0 + n."""
+        k = np.ascontiguousarray(k, dtype=np.float32)
+        v = np.ascontiguousarray(v, dtype=np.float32)
+        assert k.shape == v.shape and k.shape[0] == self.cfg.n_layers and k.shape[2] == self.cfg.kv_dim
+        self._check(lib.bh_model_kv_write(self.m, slot, row0, k.shape[1], ptr(k), ptr(v)))
+
+    def seq_len(self, slot):
+        n = ctypes.c_int64()
+        self._check(lib.bh_model_seq_len(self.m, slot, ctypes.byref(n)))
+        return n.value
 
     def seq_open(self, slot, capacity):
         self._check(lib.bh_model_seq_open(self.m, slot, capacity))

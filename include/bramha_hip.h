@@ -191,6 +191,25 @@ void bh_model_destroy(bh_model* m);
  * LM head; without it the head is the embedding (cpu_engine.rs:2449-2455). */
 int bh_model_set_weight(bh_model* m, const char* name, const void* data, size_t bytes, const void* scales,
                         size_t scale_bytes);
+/* Load a model directory in the reference's on-disk format (manifest.json + per-layer shards,
+ * written by src/bin/quantize_model.rs:284-306 and read by src/storage/tensor_db.rs:623-724):
+ * Int4PerChannel layers as {id}_u4.bin + {id}_scale.bin (cfg.wfmt must be BH_Q4_ROW for
+ * them), Int8Linear as {id}_i8.bin + {id}_scale.bin (BH_Q8_ROW), uncompressed layers as
+ * {id}.bin f32; '.' in ids becomes '_'. Shards are memory-mapped and uploaded with
+ * bh_model_set_weight; a non-empty manifest checksum must equal the shard's SHA-256.
+ * Tensors the decoder does not use are skipped; *n_loaded counts the uploaded ones. */
+int bh_model_load_dir(bh_model* m, const char* dir, int* n_loaded);
+/* KV persistence (the prefix cache of src/inference/paged_kv/prefix_cache.rs:37-120 keeps per
+ * layer the flat LayerKvCache vectors, cpu_engine.rs:1720-1755): copy rows [row0, row0 + n) of
+ * an open slot between the device cache and host f32 arrays k, v [n_layers][n][n_kv*head_dim].
+ * kv_read needs row0 + n <= the slot's length; kv_write needs row0 <= the slot's length, the
+ * slot outside the decode batch and the rows inside its capacity, and sets its length to
+ * row0 + n (a following prefill continues at that position). With eviction on, rows must stay
+ * below max_context. fp16 caches convert exactly to f32 and round back on write. */
+int bh_model_kv_read(bh_model* m, int slot, int64_t row0, int64_t n, float* k_out, float* v_out);
+int bh_model_kv_write(bh_model* m, int slot, int64_t row0, int64_t n, const float* k_in, const float* v_in);
+/* Current length (rows = next position) of a slot; 0 when the slot is not open. */
+int bh_model_seq_len(bh_model* m, int slot, int64_t* len);
 /* Number of tensors still missing (0 when the model can run). */
 int bh_model_missing(bh_model* m, int* n_missing);
 /* (Re)start sequence `slot` with room for `capacity` KV rows (capacity <= max_context when
