@@ -98,6 +98,8 @@ _PROTOS = {
     "bh_model_kv_read": (c_int, [_P, c_int, c_int64, c_int64, _P, _P]),
     "bh_model_kv_write": (c_int, [_P, c_int, c_int64, c_int64, _P, _P]),
     "bh_model_seq_len": (c_int, [_P, c_int, POINTER(c_int64)]),
+    "bh_model_set_sampling": (c_int, [_P, c_float, c_int, c_uint64]),
+    "bh_sample_uniform": (c_float, [c_uint64, c_int, c_int]),
     "bh_model_destroy": (None, [_P]),
     "bh_model_set_weight": (c_int, [_P, c_char_p, _P, c_size_t, _P, c_size_t]),
     "bh_model_missing": (c_int, [_P, POINTER(c_int)]),

@@ -610,6 +610,9 @@ int bh_attn_decode(bh_ctx* ctx, const float* q, const void* k, const void* v, in
     return e == hipSuccess ? BH_OK : ctx->hip_fail(e, "attention launch");
 }
 
+// ------------------------------------------------------------ sampling draws
+float bh_sample_uniform(uint64_t seed, int slot, int pos) { return sample_uniform(seed, slot, pos); }
+
 // ------------------------------------------------------------ measurement
 }  // extern "C"
 

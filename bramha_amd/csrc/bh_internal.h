@@ -205,7 +205,24 @@ hipError_t launch_embed(const DevWeight& table, const int32_t* tok, const float*
 // per-64-row partials; bumps the penalty count of the chosen id; records it at
 // ids_cap[step[b] * batch + b] (ids_cap may be null) and advances step[b]; sets tok[b] to it and
 // pos[b] += 1; and starts the next step's residual stream from its embedding row (as launch_embed).
+// Uniform [0, 1) draw of a sampling step (24 bits of SplitMix64 over seed, slot and the
+// position of the step's input token): reproducible, unlike the reference's thread_rng.
+__host__ __device__ inline float sample_uniform(uint64_t seed, int slot, int pos) {
+    uint64_t z = seed ^ ((uint64_t)(uint32_t)slot << 32 | (uint32_t)pos);
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    return (float)(z >> 40) * (1.0f / 16777216.0f);
+}
+constexpr int SAMPLE_TOPK_MAX = 64;
+
 struct SampleArgs {
+    // temperature > 0: top-k sampling over the penalized logits (cpu_engine.rs:2998-3022)
+    float temperature = 0.f;
+    int top_k = 40;
+    uint64_t seed = 0;
+    const float* logits = nullptr;  // raw logits [batch][vocab] (temperature > 0)
     const float* part_val = nullptr;
     const int32_t* part_idx = nullptr;
     int tiles = 0, batch = 0, vocab = 0;

@@ -80,6 +80,9 @@ struct bh_model {
     const float2* rope = nullptr;
     int max_pos = 0;
     int kv_align = 8;  // rows: every sequence region starts on a multiple
+    float temperature = 0.f;  // > 0: top-k sampling instead of greedy argmax
+    int top_k = 40;
+    uint64_t seed = 0;
     void* h_stage = nullptr;  // pinned staging for small host->device copies
 
     std::vector<int64_t> off_h, cap_h;
@@ -269,6 +272,10 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
     e = timed(m, BH_K_LM_HEAD, [&] { return launch_gemv(c.head_fmt, EPI_LMHEAD, lm, st); });
     if (e != hipSuccess) return e;
     SampleArgs sa;
+    sa.temperature = m->temperature;
+    sa.top_k = m->top_k;
+    sa.seed = m->seed;
+    sa.logits = m->logits;
     sa.part_val = m->part_val;
     sa.part_idx = m->part_idx;
     sa.tiles = m->tiles_lm;
@@ -585,6 +592,19 @@ int bh_model_load_dir(bh_model* m, const char* dir, int* n_loaded) {
         std::lock_guard<std::mutex> g(m->ctx->mu);
         return m->fail(rc, err);
     }
+    return BH_OK;
+}
+
+int bh_model_set_sampling(bh_model* m, float temperature, int top_k, uint64_t seed) {
+    if (!m || !(temperature >= 0.f) || (temperature > 0.f && (top_k < 1 || top_k > SAMPLE_TOPK_MAX)))
+        return BH_ERR_INVALID;
+    std::lock_guard<std::mutex> g(m->ctx->mu);
+    if (temperature > 0.f && m->tiles_lm > 4096)
+        return m->fail(BH_ERR_UNSUPPORTED, "sampling supports vocabularies up to 262144");
+    m->temperature = temperature;
+    m->top_k = top_k;
+    m->seed = seed;
+    drop_graph(m);  // the captured step holds the old sampling arguments
     return BH_OK;
 }
 

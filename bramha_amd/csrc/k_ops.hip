@@ -131,11 +131,121 @@ __global__ void __launch_bounds__(256) k_embed(const DevWeight t, const int32_t*
 // End of a decode step for batch entry b = blockIdx.x: the first-max argmax over the LM head's
 // per-tile partials (cpu_engine.rs:3024-3031; ties keep the lowest id), the penalty count of the
 // chosen id, the id capture, the next token and position, and the next step's residual stream.
+// Sort keys so that the larger value comes first, equal values by ascending index (the order of
+// the reference's stable sort by probability). n is a power of two; all threads take part.
+__device__ __forceinline__ bool sorts_before(float va, int ia, float vb, int ib) {
+    return va > vb || (va == vb && ia < ib);
+}
+__device__ void bitonic_sort(float* v, int* id, int n) {
+    for (int k = 2; k <= n; k <<= 1)
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int i = threadIdx.x; i < n; i += blockDim.x) {
+                const int l = i ^ j;
+                if (l <= i) continue;
+                const bool up = (i & k) == 0;
+                const bool swap = up ? sorts_before(v[l], id[l], v[i], id[i]) : sorts_before(v[i], id[i], v[l], id[l]);
+                if (swap) {
+                    const float tv = v[i];
+                    v[i] = v[l];
+                    v[l] = tv;
+                    const int ti = id[i];
+                    id[i] = id[l];
+                    id[l] = ti;
+                }
+            }
+            __syncthreads();
+        }
+}
+
+constexpr int SORT_N = 4096;  // tiles of 64 logits for vocabularies up to 262144; 64 x top_k candidates
+
+// Top-k sampling of entry b (temperature > 0): the k largest penalized logits lie in the k tiles
+// with the largest tile maxima (each of those k logits is at most its tile's maximum), so the
+// tile maxima are sorted first, the k best tiles' 64 k penalized logits second; then
+// p_i = exp(l_i/T - l_0/T) / sum over the k, and the first i whose cumulative p reaches the draw
+// r is chosen (the first one if rounding leaves every cumulative sum below r). The reference
+// normalises over the whole vocabulary first and again over the k (cpu_engine.rs:3003-3014);
+// both give the same top-k distribution.
+__device__ int sample_topk(const SampleArgs& a, int b, int slot, int pos, float* v, int* id) {
+    __shared__ int tsel[SAMPLE_TOPK_MAX];
+    __shared__ int s_pick;
+    const int K = a.top_k;
+    for (int i = threadIdx.x; i < SORT_N; i += blockDim.x) {
+        v[i] = i < a.tiles ? a.part_val[(int64_t)b * a.tiles + i] : -INFINITY;
+        id[i] = i < a.tiles ? i : 0x7fffffff;
+    }
+    __syncthreads();
+    bitonic_sort(v, id, SORT_N);
+    if (threadIdx.x < K) tsel[threadIdx.x] = id[threadIdx.x];
+    __syncthreads();
+    const uint16_t* pen = a.pen + (int64_t)slot * a.vocab;
+    for (int e = threadIdx.x; e < SORT_N; e += blockDim.x) {
+        float val = -INFINITY;
+        int n = 0x7fffffff;
+        if (e < K * 64) {
+            const int tile = tsel[e / 64];
+            const int nn = tile == 0x7fffffff ? a.vocab : tile * 64 + e % 64;
+            if (nn < a.vocab) {
+                val = a.logits[(int64_t)b * a.vocab + nn];
+                for (int c = pen[nn]; c > 0; --c) val = val > 0.f ? val / 1.15f : val * 1.15f;
+                if (!(val > -INFINITY)) val = -INFINITY;  // NaN is never chosen
+                n = nn;
+            }
+        }
+        v[e] = val;
+        id[e] = n;
+    }
+    __syncthreads();
+    bitonic_sort(v, id, SORT_N);
+    if (threadIdx.x == 0) {
+        const float inv = 1.0f / a.temperature;
+        const float mx = v[0] * inv;
+        float ex[SAMPLE_TOPK_MAX];
+        float sum = 0.f;
+        for (int i = 0; i < K; ++i) {
+            ex[i] = v[i] > -INFINITY ? expf(v[i] * inv - mx) : 0.f;
+            sum += ex[i];
+        }
+        const float r = sample_uniform(a.seed, slot, pos);
+        int pick = id[0];
+        float cum = 0.f;
+        for (int i = 0; i < K; ++i) {
+            cum += ex[i] / sum;
+            if (r <= cum) {
+                pick = id[i];
+                break;
+            }
+        }
+        s_pick = pick;
+    }
+    __syncthreads();
+    return s_pick;
+}
+
 __global__ void __launch_bounds__(256) k_sample(const SampleArgs a, const DevWeight t) {
     __shared__ float sv[4];
     __shared__ int si[4];
     __shared__ int s_id;
+    __shared__ float sort_v[SORT_N];
+    __shared__ int sort_i[SORT_N];
     const int b = blockIdx.x;
+    if (a.temperature > 0.f) {
+        const int slot = a.slot[b];
+        const int idx = sample_topk(a, b, slot, a.pos[b], sort_v, sort_i);
+        if (threadIdx.x == 0) {
+            uint16_t* c = a.pen + (int64_t)slot * a.vocab + idx;
+            if (*c < 0xFFFF) *c = *c + 1;
+            if (a.ids_cap) {
+                const int s = a.step[b];
+                a.ids_cap[(int64_t)s * a.batch + b] = (uint32_t)idx;
+                a.step[b] = s + 1;
+            }
+            a.tok[b] = idx;
+            a.pos[b] = a.pos[b] + 1;
+        }
+        embed_stream(t, idx, a.w0, a.x, a.xw, a.ssq, a.ssq_tiles, b);
+        return;
+    }
     float v = -INFINITY;
     int idx = 0x7fffffff;
     for (int i = threadIdx.x; i < a.tiles; i += blockDim.x) {
@@ -261,6 +371,8 @@ hipError_t launch_embed(const DevWeight& t, const int32_t* tok, const float* w0,
 hipError_t launch_sample(const SampleArgs& a, hipStream_t st) {
     if (a.batch <= 0) return hipSuccess;
     if (!a.table || a.ssq_tiles != (int)((a.table->k + 63) / 64) || (a.ids_cap && !a.step)) return hipErrorInvalidValue;
+    if (a.temperature > 0.f && (!a.logits || a.top_k < 1 || a.top_k > SAMPLE_TOPK_MAX || a.tiles > SORT_N))
+        return hipErrorInvalidValue;
     launch_kernel(k_sample, dim3(a.batch), dim3(256), 0, st, a, *a.table);
     return hipGetLastError();
 }

@@ -196,6 +196,11 @@ class HipDecoder:
         assert k.shape == v.shape and k.shape[0] == self.cfg.n_layers and k.shape[2] == self.cfg.kv_dim
         self._check(lib.bh_model_kv_write(self.m, slot, row0, k.shape[1], ptr(k), ptr(v)))
 
+    def set_sampling(self, temperature, top_k=40, seed=0):
+        """temperature 0: greedy (default); > 0: top-k sampling on the device
+        (bh_model_set_sampling)."""
+        self._check(lib.bh_model_set_sampling(self.m, float(temperature), int(top_k), int(seed)))
+
     def seq_len(self, slot):
         n = ctypes.c_int64()
         self._check(lib.bh_model_seq_len(self.m, slot, ctypes.byref(n)))

@@ -210,6 +210,15 @@ int bh_model_kv_read(bh_model* m, int slot, int64_t row0, int64_t n, float* k_ou
 int bh_model_kv_write(bh_model* m, int slot, int64_t row0, int64_t n, const float* k_in, const float* v_in);
 /* Current length (rows = next position) of a slot; 0 when the slot is not open. */
 int bh_model_seq_len(bh_model* m, int slot, int64_t* len);
+/* Token selection of the decode step (cpu_engine.rs:2984-3031). temperature 0 (the default):
+ * greedy first-max argmax of the penalized logits. temperature > 0: the reference's top-k
+ * sampling — logits / temperature, softmax, the top_k (1..64; the reference uses 40) most likely
+ * ids renormalised, the first id whose cumulative probability reaches a uniform draw r — on the
+ * device, with r = bh_sample_uniform(seed, slot, position of the step's input token) instead of
+ * the reference's unseeded thread_rng. The repetition penalty and EOS handling are unchanged. */
+int bh_model_set_sampling(bh_model* m, float temperature, int top_k, uint64_t seed);
+/* The draw used by a sampling step (no counterpart in the reference; for reproducing a run). */
+float bh_sample_uniform(uint64_t seed, int slot, int pos);
 /* Number of tensors still missing (0 when the model can run). */
 int bh_model_missing(bh_model* m, int* n_missing);
 /* (Re)start sequence `slot` with room for `capacity` KV rows (capacity <= max_context when

@@ -61,6 +61,7 @@ _PROTOS = {
     "orc_attn_prefill": (None, [_P, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int64, _P]),
     "orc_silu_mul": (None, [_P, _P, c_int64, _P]),
     "orc_penalize_argmax": (c_int64, [_P, c_int64, _P, c_int64]),
+    "orc_sample_topk": (c_int64, [_P, c_int64, c_float, c_int, c_float]),
     "orc_model_create": (c_void_p, [POINTER(orc_config)]),
     "orc_model_destroy": (None, [_P]),
     "orc_model_set": (c_int, [_P, ctypes.c_char_p, _P, _P]),
@@ -226,6 +227,12 @@ def penalize_argmax(logits, generated):
     g = np.ascontiguousarray(generated, np.uint32)
     idx = _lib.orc_penalize_argmax(_p(lg), lg.size, _p(g), g.size)
     return int(idx), lg
+
+
+def sample_topk(penalized, temperature, top_k, r):
+    """The reference's temperature / top-k choice over penalized logits for a given draw r."""
+    lg = _f32(penalized)
+    return int(_lib.orc_sample_topk(_p(lg), lg.size, float(temperature), int(top_k), float(r)))
 
 
 def num_threads():

@@ -648,6 +648,49 @@ int64_t orc_penalize_argmax(float* logits, int64_t V, const uint32_t* gen, int64
     return best;
 }
 
+// The temperature > 0 branch of the token choice (cpu_engine.rs:2998-3022) over already
+// penalized logits, with the uniform draw r passed in (the reference takes it from thread_rng):
+// divide by the temperature, softmax over the whole vocabulary, stable sort by probability
+// (descending; incomparable pairs keep their order), keep top_k, renormalise, and return the first
+// id whose cumulative probability reaches r (the most likely one if none does).
+int64_t orc_sample_topk(const float* penalized, int64_t V, float temperature, int top_k, float r) {
+    std::vector<float> v(penalized, penalized + V);
+    for (auto& x : v) x /= temperature;
+    float mx = -INFINITY;
+    for (float x : v) mx = std::isnan(mx) ? x : (std::isnan(x) ? mx : std::max(mx, x));  // f32::max
+    std::vector<float> ex(V);
+    float sum = 0.f;
+    for (int64_t i = 0; i < V; ++i) {
+        ex[i] = expf(v[i] - mx);
+        sum += ex[i];
+    }
+    if (sum > 0.f)
+        for (auto& e : ex) e /= sum;
+    std::vector<int64_t> idx(V);
+    for (int64_t i = 0; i < V; ++i) idx[i] = i;
+    // the reference's comparator treats NaN as equal to everything; NaN probabilities (from NaN
+    // logits) sort here as 0 so that the order stays a strict weak ordering
+    std::vector<float> key(ex);
+    for (auto& k : key)
+        if (std::isnan(k)) k = 0.f;
+    std::stable_sort(idx.begin(), idx.end(), [&](int64_t a, int64_t b) { return key[a] > key[b]; });
+    if ((int64_t)top_k < V) idx.resize(top_k);
+    float top_sum = 0.f;
+    for (int64_t i : idx) top_sum += ex[i];
+    std::vector<float> p(idx.size());
+    for (size_t i = 0; i < idx.size(); ++i) p[i] = top_sum > 0.f ? ex[idx[i]] / top_sum : ex[idx[i]];
+    int64_t selected = idx[0];
+    float cum = 0.f;
+    for (size_t i = 0; i < idx.size(); ++i) {
+        cum += p[i];
+        if (r <= cum) {
+            selected = idx[i];
+            break;
+        }
+    }
+    return selected;
+}
+
 // generate_cpu_inner_logits with CPU-only mode and temperature 0:
 // prefill of tokens [0, n-1) in chunks of 64 (cpu_engine.rs:2586-2757), then the
 // single-token decode loop (:2788-3064): embedding row id % V, 24 x [norm, QKV

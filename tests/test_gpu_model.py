@@ -226,3 +226,39 @@ def test_qwen2_0_5b_4bit_parity(plane):
     for t in range(n):
         assert np.max(np.abs(glg[t] - olg[t])) <= 2e-2, t
         assert rel_l2(glg[t], olg[t]) <= 1e-3, t
+
+
+@pytest.mark.parametrize("temperature,top_k", [(0.8, 40), (1.5, 5)])
+def test_device_sampling_matches_reference_rule(plane, temperature, top_k):
+    """Top-k temperature sampling on the device: at every step the chosen id is the oracle's
+    choice (the reference rule, cpu_engine.rs:2998-3022) over the same step's penalized logits
+    and the same draw r = bh_sample_uniform(seed, slot, position); steps whose r lies within
+    1e-5 of a cumulative boundary are numerical ties and not compared."""
+    from bramha_amd import _lib
+
+    cfg = tiny_cfg(Q4_G32, Q4_G32, gqa7=True)
+    _, gm = _pair(plane, cfg, seed=71)
+    seed = 1234
+    gm.set_sampling(temperature, top_k, seed)
+    p = prompt(7, cfg.vocab, seed=72)
+    ids, lg = gm.generate(p, 24, want_logits=True)
+    assert len(ids) >= 1
+    gen = []
+    checked = 0
+    for t in range(len(ids)):
+        pen = lg[t].copy()
+        for g in gen:
+            pen[g] = pen[g] / 1.15 if pen[g] > 0 else pen[g] * 1.15
+        r = _lib.lib.bh_sample_uniform(seed, 0, len(p) - 1 + t)
+        want = oracle.sample_topk(pen, temperature, top_k, r)
+        near = any(abs(oracle.sample_topk(pen, temperature, top_k, r + d) - want) > 0 for d in (-1e-5, 1e-5))
+        if not near:
+            assert ids[t] == want, (t, ids[t], want, r)
+            checked += 1
+        gen.append(int(ids[t]))
+    assert checked >= len(ids) - 2
+    # back to greedy: the default decode again
+    gm.set_sampling(0.0)
+    g1 = gm.generate(p, 8)
+    om, _ = _pair(plane, cfg, seed=71)
+    assert np.array_equal(g1, om.generate(p, 8))

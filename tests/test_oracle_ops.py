@@ -165,3 +165,24 @@ def test_penalty_and_argmax():
     assert idx == 0
     idx, pl = oracle.penalize_argmax(lg, [99])  # ids past the vocab are ignored
     assert idx == 1 and np.array_equal(pl, lg)
+
+
+def test_sample_topk_reference_rules():
+    """The temperature branch (cpu_engine.rs:2998-3022) for a given draw r: top_k = 1 is the
+    argmax; r = 0 the most likely id; ties keep index order; sweeping r over [0, 1) visits the
+    top-k ids with their renormalised probabilities."""
+    rng = np.random.default_rng(7)
+    lg = (rng.standard_normal(300) * 2).astype(np.float32)
+    order = np.argsort(-lg, kind="stable")
+    assert oracle.sample_topk(lg, 0.7, 1, 0.99) == int(order[0])
+    assert oracle.sample_topk(lg, 0.7, 40, 0.0) == int(order[0])
+    tie = np.zeros(50, np.float32)
+    assert [oracle.sample_topk(tie, 1.0, 5, r) for r in (0.0, 0.25, 0.45, 0.65, 0.85)] == [0, 1, 2, 3, 4]
+    T, k = 0.8, 6
+    p = np.exp(lg[order[:k]].astype(np.float64) / T - lg[order[0]] / T)
+    p /= p.sum()
+    draws = (np.arange(20000) + 0.5) / 20000
+    got = np.array([oracle.sample_topk(lg, T, k, r) for r in draws])
+    for i in range(k):
+        assert abs(np.mean(got == order[i]) - p[i]) < 2e-3
+    assert set(got) <= set(order[:k].tolist())
