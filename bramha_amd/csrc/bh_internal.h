@@ -257,7 +257,14 @@ struct AttnArgs {
     int prefill = 0;
     float* part_o = nullptr;           // [batch][nq][splits][hd]
     float* part_ml = nullptr;          // [batch][nq][splits][2]
+    // Decode of the device model (fp16 cache, batch <= ATTN_STATIC_B): the entries' first KV
+    // rows and the smallest region capacity as launch arguments, fixed while the batch is, so
+    // each wave requests its first K/V tile before the positions arrive. 0: read boff.
+    int static_off = 0;
+    int64_t cap_rows = 0;
+    int64_t off_val[32] = {};
 };
+constexpr int ATTN_STATIC_B = 32;
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
 // Head layouts the attention kernel is built for: hd 64/128, n_q/n_kv in {1, 2, 4, 7, 8}.
 bool attn_supported(int nq, int nkv, int hd);

@@ -228,6 +228,14 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
         at.part_ml = m->attn_part + m->attn_rows * c.n_heads * m->max_splits * c.head_dim;
         at.cnt = m->attn_cnt;
         at.prefill = decode ? 0 : 1;
+        if (decode && c.kv_f16 && M <= ATTN_STATIC_B) {
+            at.static_off = 1;
+            at.cap_rows = INT64_MAX;
+            for (int b = 0; b < M; ++b) {
+                at.off_val[b] = m->off_h[m->bslots[b]];
+                at.cap_rows = std::min<int64_t>(at.cap_rows, m->cap_h[m->bslots[b]]);
+            }
+        }
         e = timed(m, BH_K_ATTN, [&] { return launch_attention(at, st); });
         if (e != hipSuccess) break;
         GemvArgs o;
@@ -772,7 +780,7 @@ int bh_model_decode_setup(bh_model* m, int batch, const int32_t* slots, const ui
             return m->fail(BH_ERR_INVALID, "decode slot is not open");
         if (seen[slots[b]]++) return m->fail(BH_ERR_INVALID, "a slot appears twice in the decode batch");
     }
-    if (batch != m->B) drop_graph(m);
+    drop_graph(m);  // the captured step holds the entries' KV offsets as launch arguments
     m->B = batch;
     m->bslots.assign(slots, slots + batch);
     for (int b = 0; b < batch; ++b) {
@@ -790,6 +798,7 @@ int bh_model_decode_replace(bh_model* m, int b, int slot, uint32_t first_token) 
     for (int i = 0; i < m->B; ++i)
         if (i != b && m->bslots[i] == slot) return m->fail(BH_ERR_INVALID, "slot already in the batch");
     m->bslots[b] = slot;
+    drop_graph(m);  // the captured step holds the entries' KV offsets as launch arguments
     hipError_t e = set_entry(m, b, slot, first_token);
     return e == hipSuccess ? BH_OK : m->ctx->hip_fail(e, "decode_replace");
 }

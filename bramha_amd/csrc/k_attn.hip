@@ -405,6 +405,35 @@ struct AttnWave {
         }
     }
 
+    // The tile at t0 with every row loaded (rows past r1 included: the caller guarantees they
+    // are inside the region); used before r1 is known, then zero_tail clears the V rows past it.
+    __device__ __forceinline__ void load_full(KvTile<HD>& T, int t0) const {
+        const int lane = threadIdx.x & 63;
+        const __half* kb = Kh + (off + t0) * HD;
+        const __half* vb = Vh + (off + t0) * HD;
+#pragma unroll
+        for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+            for (int kc = 0; kc < KC; ++kc) T.k[blk][kc] = *(const half8*)(kb + ((blk * KC + kc) * 64 + lane) * 8);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int db = 0; db < DB; ++db) T.v[j][db] = *(const half8*)(vb + ((j * DB + db) * 64 + lane) * 8);
+    }
+    // Zero the V rows at or past r1 (their P is 0, but 0 * NaN of a stale row would not be).
+    // K rows past r1 need nothing: their scores are replaced, not multiplied.
+    __device__ __forceinline__ void zero_tail(KvTile<HD>& T, int t0) const {
+        const int lg = (threadIdx.x & 63) >> 4;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int tg = t0 + 32 * j + 8 * lg;
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) T.v[j][db][e] = tg + e < r1 ? T.v[j][db][e] : (_Float16)0.f;
+        }
+    }
+
     __device__ __forceinline__ void start() {
         const int t = r0 + (int)(threadIdx.x >> 6) * TR;
         if (t < r1) load_tile(A, t);
@@ -521,7 +550,16 @@ __global__ void __launch_bounds__(64 * NW) k_attn_mf(const AttnArgs a) {
         const int i = threadIdx.x + k * NT;
         qreg[k] = i / HD < G ? a.q[((int64_t)b * a.nq + h * G) * HD + i] : 0.f;
     }
-    const int64_t off = a.boff[b];
+    const int64_t off = a.static_off ? a.off_val[b] : a.boff[b];
+    const int r0 = sp * a.split_rows;
+    const int64_t head = (int64_t)h * a.kv.kv_rows * HD;
+    AttnWave<HD, NW, false> aw{(const __half*)a.kv.k + head, (const __half*)a.kv.v + head, off,
+                               (off & 63) == 0 && (a.kv.kv_rows & 7) == 0, ((off | a.kv.kv_rows) & 7) == 0,
+                               r0, 0, 0, 0};
+    // first tile requested before the sequence length is known, when it lies in the region
+    const int tfirst = r0 + wave * AttnWave<HD, NW, false>::TR;
+    const bool spec = a.static_off && aw.tiled && tfirst + AttnWave<HD, NW, false>::TR <= a.cap_rows;
+    if (spec) aw.load_full(aw.A, tfirst);
     int len;
     if (a.seq_len) {
         len = a.seq_len[b];
@@ -529,13 +567,10 @@ __global__ void __launch_bounds__(64 * NW) k_attn_mf(const AttnArgs a) {
         len = a.pos[b] + 1;
         if (a.kv.max_context > 0) len = min(len, a.kv.max_context);
     }
-    const int r0 = sp * a.split_rows;
     const int r1 = min(len, r0 + a.split_rows);
-    const int64_t head = (int64_t)h * a.kv.kv_rows * HD;
-    AttnWave<HD, NW, false> aw{(const __half*)a.kv.k + head, (const __half*)a.kv.v + head, off,
-                               (off & 63) == 0 && (a.kv.kv_rows & 7) == 0, ((off | a.kv.kv_rows) & 7) == 0,
-                               r0, r1, r1, r1};
-    aw.start();
+    aw.r1 = aw.lim = aw.lim_all = r1;
+    if (!spec) aw.start();
+    else if (tfirst < r1 && tfirst + AttnWave<HD, NW, false>::TR > r1) aw.zero_tail(aw.A, tfirst);
 
     // q rows into LDS, then Q^T as the B operand:
     // lane (lr, lg) holds head lr, head-dim kc*32 + 8lg .. +7
