@@ -89,9 +89,133 @@ __device__ __forceinline__ bool split_reduce(const GemvArgs& a, float* comb, int
     return true;
 }
 
+// Epilogue operands of a batch-1 launch for the weight row row0 + threadIdx.x (threadIdx.x <
+// ROWS: the thread that finishes that row), loaded at the start of the kernel so that their
+// latency — including the position -> RoPE table and slot -> penalty chains — hides under the
+// weight stream instead of following it.
+template <int EPI>
+struct EpiPre {
+    float x0 = 0.f, w1 = 0.f, bias = 0.f, pbias = 0.f;  // residual, next norm weight, biases
+    float2 cs = {1.f, 0.f};                             // RoPE (cos, sin)
+    int64_t kvrow = 0;                                  // KV row of the token
+    int cnt = 0;                                        // penalty count
+    __device__ __forceinline__ void load(const GemvArgs& a, int64_t row0) {
+        const int64_t nn = row0 + threadIdx.x;
+        if (nn >= a.N) return;
+        if constexpr (EPI == EPI_STORE) {
+            if (a.bias) bias = a.bias[nn];
+        } else if constexpr (EPI == EPI_RESNORM) {
+            x0 = a.y[nn];
+            w1 = a.wnext[nn];
+            if (a.bias) bias = a.bias[nn];
+        } else if constexpr (EPI == EPI_QKV) {
+            const int half = a.hd >> 1;
+            const int sec = nn < a.qd ? 0 : (nn < a.qd + a.kd ? 1 : 2);
+            const int loc = (int)nn - (sec == 0 ? 0 : (sec == 1 ? a.qd : a.qd + a.kd));
+            const int d = loc % a.hd;
+            const int p = a.pos[0];
+            if (a.bias) {
+                bias = a.bias[nn];
+                if (sec < 2) pbias = a.bias[nn + (d < half ? half : -half)];
+            }
+            if (sec < 2) cs = a.rope[(int64_t)p * half + (d < half ? d : d - half)];
+            if (sec > 0) kvrow = a.boff[0] + kv_phys_row(a.kv, p);
+        } else if constexpr (EPI == EPI_LMHEAD) {
+            cnt = a.pen[(int64_t)a.slot[0] * a.vocab + nn];
+        }
+    }
+};
+
 template <int FMT, int B, int EPI, int ROWS>
 __device__ __forceinline__ void run_epilogue(const GemvArgs& a, const float* fin, float* scratch, const float* rn,
-                                             int64_t row0) {
+                                             int64_t row0, const EpiPre<EPI>* pre = nullptr) {
+    if constexpr (B == 1) {
+        if (pre) {  // batch 1 with prefetched operands: thread r finishes row row0 + r
+            const int lane = threadIdx.x & 63;
+            const int wave = threadIdx.x >> 6;
+            const int nwaves = blockDim.x >> 6;
+            const int rr = threadIdx.x;
+            const int64_t nn = row0 + rr;
+            const bool ok = rr < ROWS && nn < a.N;
+            if constexpr (EPI == EPI_STORE) {
+                if (ok) a.y[nn] = fin[rr] * row_scale<FMT>(a.S, nn) * rn[0] + pre->bias;
+            } else if constexpr (EPI == EPI_RESNORM) {
+                float sq = 0.f;
+                if (ok) {
+                    const float v = pre->x0 + (fin[rr] * row_scale<FMT>(a.S, nn) + pre->bias);
+                    a.y[nn] = v;
+                    a.xw_out[nn] = v * pre->w1;
+                    sq = v * v;
+                }
+                if (rr < ROWS) scratch[rr] = sq;
+                __syncthreads();
+                constexpr int SUB = ROWS / 64;
+                for (int q = wave; q < SUB; q += nwaves) {
+                    const float t = wave_sum64(scratch[q * 64 + lane]);
+                    const int64_t tile = row0 / 64 + q;
+                    if (lane == 0 && tile < a.ssq_tiles) a.ssq_out[tile] = t;
+                }
+            } else if constexpr (EPI == EPI_SILU) {
+                if (ok) {
+                    const float g = fin[rr] * row_scale<FMT>(a.S, nn) * rn[0];
+                    const float u = fin[ROWS + rr] * row_scale<FMT>(a.S2, nn) * rn[0];
+                    a.y[nn] = g * (1.0f / (1.0f + expf(-g))) * u;
+                }
+            } else if constexpr (EPI == EPI_QKV) {
+                if (ok) {
+                    const int half = a.hd >> 1;
+                    float val = fin[rr] * row_scale<FMT>(a.S, nn) * rn[0] + pre->bias;
+                    const int sec = nn < a.qd ? 0 : (nn < a.qd + a.kd ? 1 : 2);
+                    const int loc = (int)nn - (sec == 0 ? 0 : (sec == 1 ? a.qd : a.qd + a.kd));
+                    const int hh = loc / a.hd, d = loc % a.hd;
+                    if (sec < 2) {  // rotate-half RoPE (apply_rope_cpu, cpu_engine.rs:1682-1699)
+                        const int dp = d < half ? half : -half;
+                        const float pv = fin[rr + dp] * row_scale<FMT>(a.S, nn + dp) * rn[0] + pre->pbias;
+                        val = d < half ? (val * pre->cs.x - pv * pre->cs.y) : (val * pre->cs.x + pv * pre->cs.y);
+                    }
+                    if (sec == 0) {
+                        a.y[nn] = val;
+                    } else {
+                        const int64_t head = (int64_t)hh * a.kv.kv_rows * a.hd;
+                        if (a.kv.kv_f16) {
+                            if (sec == 1) ((__half*)a.kv.k)[head + kv_k_off(pre->kvrow, d, a.hd)] = __float2half(val);
+                            else ((__half*)a.kv.v)[head + kv_v_off(pre->kvrow, d, a.hd)] = __float2half(val);
+                        } else {
+                            ((float*)(sec == 1 ? a.kv.k : a.kv.v))[head + pre->kvrow * a.hd + d] = val;
+                        }
+                    }
+                }
+            } else if constexpr (EPI == EPI_LMHEAD) {
+                float pv = -INFINITY;
+                if (ok) {
+                    float v = fin[rr] * row_scale<FMT>(a.S, nn) * rn[0];
+                    a.y[nn] = v;
+                    for (int t = 0; t < pre->cnt; ++t) v = v > 0.f ? v / 1.15f : v * 1.15f;
+                    pv = v > -INFINITY ? v : -INFINITY;
+                }
+                if (rr < ROWS) scratch[rr] = pv;
+                __syncthreads();
+                constexpr int SUB = ROWS / 64;
+                const int tiles64 = (int)((a.n_pad + 63) / 64);
+                for (int q = wave; q < SUB; q += nwaves) {
+                    float v = scratch[q * 64 + lane];
+                    int idx = v > -INFINITY ? (int)(row0 + q * 64 + lane) : 0x7fffffff;
+#pragma unroll
+                    for (int off = 32; off > 0; off >>= 1) {
+                        const float ov = __shfl_xor(v, off);
+                        const int oi = __shfl_xor(idx, off);
+                        argmax_combine(v, idx, ov, oi);
+                    }
+                    const int64_t t64 = row0 / 64 + q;
+                    if (lane == 0 && t64 < tiles64) {
+                        a.part_val[t64] = v;
+                        a.part_idx[t64] = idx;
+                    }
+                }
+            }
+            return;
+        }
+    }
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int nwaves = blockDim.x >> 6;

@@ -114,6 +114,7 @@ __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
     // Loads use a clamped row so they are unconditional and in bounds; rows past n_pad (RW = 2
     // tiles) compute values the epilogue never stores.
     const int64_t nl = row_ok ? n : (int64_t)a.n_pad - 1;
+    EpiPre<EPI> pre;
 
     {
         // Weight and scale loads are raw buffer loads: an SGPR resource per matrix, the lane's row
@@ -156,6 +157,8 @@ __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
                     touch += a.x[(int64_t)bb * a.ldx + wc0 * E + i2];
         }
         load_rnorm<B>(a, rn);
+        if constexpr (B == 1)
+            if (threadIdx.x < ROWS) pre.load(a, (int64_t)tile * ROWS);
 
         float acc[NACC][B];
 #pragma unroll
@@ -215,7 +218,7 @@ __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
     }
     if (ksw > 1 && !split_reduce<TOT>(a, comb, tile, kws)) return;
     __syncthreads();
-    run_epilogue<FMT, B, EPI, ROWS>(a, comb, comb + TOT, rn, (int64_t)tile * ROWS);
+    run_epilogue<FMT, B, EPI, ROWS>(a, comb, comb + TOT, rn, (int64_t)tile * ROWS, B == 1 ? &pre : nullptr);
 }
 
 template <int FMT, int B, int EPI, int RW, int U>
