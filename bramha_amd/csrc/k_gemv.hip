@@ -4,20 +4,11 @@
 // y[j] = scale[j] * sum_i h[i] * q[j][i] for the row formats, plain dot for F32.
 // The Q4_G32 format applies its fp16 scale per group of 32 (one 16-byte chunk).
 //
-// Design (HBM-bound, no MFMA): the weight is stored K-major in 16-byte chunks
-// (bh_internal.h, "KM16"), so each lane owns one output row and a wavefront
-// streams 1 KiB of contiguous weight bytes per chunk step with one
-// global_load_dwordx4 per lane. The activations of a chunk are identical for all
-// 64 lanes, so they arrive through scalar loads (s_load_dwordx16) and enter the
-// FMAs as SGPR operands: no LDS traffic and no cross-lane reduction in the main loop.
-// Nibbles are decoded as signed int4 (q ^ 8 == q - 8 in two's complement) shifted
-// into the top of a byte and converted with the SDWA sign-extending byte convert:
-// one VALU op per element plus three bit ops per 8 elements; the factor 16 is
-// folded into the scale. The chunk loop is software-pipelined (the next batch of
-// chunks is in flight while the current one is converted), and the first batch is
-// requested before anything else the kernel loads, so the weight latency overlaps the
-// per-token norm factors and epilogue operands. Waves of a workgroup split K and combine
-// in LDS in a fixed order, so results are deterministic without atomics.
+// Design (HBM-bound, no MFMA): one lane per output row streaming the K-major 16-byte chunks
+// with SGPR activations (k_stream.h). The first stage of weight loads is requested before
+// anything else the kernel loads, so the weight latency overlaps the per-token norm factors and
+// epilogue operands. Waves of a workgroup split K and combine in LDS in a fixed order, so
+// results are deterministic without atomics.
 // Epilogues fuse the RMSNorm factor, bias, residual add (with the next norm's inputs),
 // SiLU gate, RoPE + KV-cache append, and the LM-head repetition penalty + argmax.
 #include "bh_internal.h"
@@ -25,62 +16,10 @@
 #include <hip/hip_fp16.h>
 
 #include "k_epilogue.h"
+#include "k_stream.h"
 
 namespace bh {
 namespace {
-
-// Signed byte SEL of v converted to f32 (v_cvt_f32_i32 with SDWA sign extension).
-template <int SEL>
-__device__ __forceinline__ float sb2f(uint32_t v) {
-    float r;
-    if constexpr (SEL == 0)
-        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(r) : "v"(v));
-    else if constexpr (SEL == 1)
-        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(r) : "v"(v));
-    else if constexpr (SEL == 2)
-        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(r) : "v"(v));
-    else
-        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(r) : "v"(v));
-    return r;
-}
-
-template <int FMT>
-struct Fmt {
-    static constexpr int E = (FMT == BH_Q4_ROW || FMT == BH_Q4_G32) ? 32 : (FMT == BH_Q8_ROW ? 16 : 4);
-};
-
-// Decode one 16-byte chunk into E values. Q4 values come out as 16*(q-8),
-// Q8 values as q, F32 as is.
-template <int FMT>
-__device__ __forceinline__ void decode(const uint4 q, float* v) {
-    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-    if constexpr (FMT == BH_Q4_ROW || FMT == BH_Q4_G32) {
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            const uint32_t hi = (w[d] & 0xF0F0F0F0u) ^ 0x80808080u;         // even elements
-            const uint32_t lo = ((w[d] << 4) & 0xF0F0F0F0u) ^ 0x80808080u;  // odd elements
-            v[8 * d + 0] = sb2f<0>(hi);
-            v[8 * d + 1] = sb2f<0>(lo);
-            v[8 * d + 2] = sb2f<1>(hi);
-            v[8 * d + 3] = sb2f<1>(lo);
-            v[8 * d + 4] = sb2f<2>(hi);
-            v[8 * d + 5] = sb2f<2>(lo);
-            v[8 * d + 6] = sb2f<3>(hi);
-            v[8 * d + 7] = sb2f<3>(lo);
-        }
-    } else if constexpr (FMT == BH_Q8_ROW) {
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            v[4 * d + 0] = sb2f<0>(w[d]);
-            v[4 * d + 1] = sb2f<1>(w[d]);
-            v[4 * d + 2] = sb2f<2>(w[d]);
-            v[4 * d + 3] = sb2f<3>(w[d]);
-        }
-    } else {
-#pragma unroll
-        for (int d = 0; d < 4; ++d) v[d] = __uint_as_float(w[d]);
-    }
-}
 
 template <int FMT, int B, int EPI, int RW, int U, int CP>
 __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
@@ -117,91 +56,16 @@ __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
     EpiPre<EPI> pre;
 
     {
-        // Weight and scale loads are raw buffer loads: an SGPR resource per matrix, the lane's row
-        // as the VGPR offset and the chunk as the (uniform) SGPR offset, so a stage costs no
-        // per-load address arithmetic. Every load of a stage is unconditional (chunk index
-        // clamped to the wave's last chunk, scale kept as raw fp16 bits) so all of a stage's
-        // loads are in flight before the first of them is waited on.
-        __amdgpu_buffer_rsrc_t rW[NACC], rS[NACC];
-        rW[0] = __builtin_amdgcn_make_buffer_rsrc((void*)a.W, (short)0, a.C * a.n_pad * 16, 0x00020000);
-        rS[0] = __builtin_amdgcn_make_buffer_rsrc((void*)a.S, (short)0, a.C * a.n_pad * 2, 0x00020000);
-        if constexpr (NACC == 2) {
-            rW[1] = __builtin_amdgcn_make_buffer_rsrc((void*)a.W2, (short)0, a.C * a.n_pad * 16, 0x00020000);
-            rS[1] = __builtin_amdgcn_make_buffer_rsrc((void*)a.S2, (short)0, a.C * a.n_pad * 2, 0x00020000);
-        }
-        const int vo_w = (int)nl * 16, vo_s = (int)nl * 2;
-        uint4 q0[NACC][U], q1[NACC][U];
-        uint16_t s0[NACC][U], s1[NACC][U];
-        auto fetch = [&](int c, uint4 (&q)[NACC][U], uint16_t (&s)[NACC][U]) {
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int cc = min(c + u, c1 - 1);
-#pragma unroll
-                for (int j = 0; j < NACC; ++j) {
-                    q[j][u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rW[j], vo_w, cc * a.n_pad * 16, CP));
-                    if constexpr (FMT == BH_Q4_G32) s[j][u] = __builtin_amdgcn_raw_buffer_load_b16(rS[j], vo_s, cc * a.n_pad * 2, CP);
-                }
-            }
-        };
-        if (c0 < c1) fetch(c0, q0, s0);
-        // The activations reach the FMAs through scalar loads issued chunk by chunk; they were
-        // just written by the previous kernel (often on another XCD), so a first touch here, one
-        // vector load per 128-byte line of the workgroup's range, brings them into L2 while the
-        // first weight stage is in flight (bs1 decode step: 1232 -> 1291 tok/s). The value is
-        // consumed only after the main loop, so nothing waits on it early.
-        float touch = 0.f;
-        {
-            const int nx = (wc1 - wc0) * E;
-            for (int bb = 0; bb < B; ++bb)
-                for (int i2 = threadIdx.x * 32; i2 < nx; i2 += blockDim.x * 32)
-                    touch += a.x[(int64_t)bb * a.ldx + wc0 * E + i2];
-        }
-        load_rnorm<B>(a, rn);
-        if constexpr (B == 1)
-            if (threadIdx.x < ROWS) pre.load(a, (int64_t)tile * ROWS);
-
         float acc[NACC][B];
-#pragma unroll
-        for (int j = 0; j < NACC; ++j)
-#pragma unroll
-            for (int b = 0; b < B; ++b) acc[j][b] = 0.f;
-
-        // Chunks past c1 (clamped re-reads of the last one) are skipped by a uniform branch that
-        // holds no vector loads, so the loads' wait counts are unaffected by it.
-        auto consume = [&](int c, const uint4 (&q)[NACC][U], const uint16_t (&s)[NACC][U]) {
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                if (c + u < c1) {
-                    const int kb = (c + u) * E;
-#pragma unroll
-                    for (int j = 0; j < NACC; ++j) {
-                        float v[E];
-                        decode<FMT>(q[j][u], v);
-#pragma unroll
-                        for (int b = 0; b < B; ++b) {
-                            const float* xb = a.x + (int64_t)b * a.ldx + kb;
-                            float p = 0.f;
-#pragma unroll
-                            for (int e = 0; e < E; ++e) p = fmaf(xb[e], v[e], p);
-                            if constexpr (FMT == BH_Q4_G32)
-                                acc[j][b] = fmaf(p, __half2float(__ushort_as_half(s[j][u])) * 0.0625f, acc[j][b]);
-                            else
-                                acc[j][b] += p;
-                        }
-                    }
-                }
-            }
-        };
-        if (c0 < c1) {
-            for (int c = c0;; c += 2 * U) {
-                fetch(c + U, q1, s1);
-                consume(c, q0, s0);
-                if (c + U >= c1) break;
-                fetch(c + 2 * U, q0, s0);
-                consume(c + U, q1, s1);
-                if (c + 2 * U >= c1) break;
-            }
-        }
+        float touch = 0.f;
+        stream_chunks<FMT, B, NACC, U, CP>(a, nl, c0, c1, acc, [&] {
+            // the activation touch (bs1 decode step: 1232 -> 1291 tok/s), the norm factors and the
+            // batch-1 epilogue operands load while the first weight stage is in flight
+            touch = touch_activations<B, E>(a, wc0, wc1);
+            load_rnorm<B>(a, rn);
+            if constexpr (B == 1)
+                if (threadIdx.x < ROWS) pre.load(a, (int64_t)tile * ROWS);
+        });
 #pragma unroll
         for (int j = 0; j < NACC; ++j)
 #pragma unroll
