@@ -786,7 +786,10 @@ __global__ void __launch_bounds__(64 * NW) k_attn_pf(const AttnArgs a) {
 template <int HD, int KVF16, int G>
 hipError_t launch_t(const AttnArgs& a, hipStream_t st) {
     if constexpr (KVF16) {
-        if (a.split_rows >= 512) launch_kernel((k_attn_mf<HD, G, 8>), dim3(a.splits, a.nkv, a.batch), dim3(512), 0, st, a);
+        // 8 waves once a split holds more than 4 tiles, so that every wave's first tile (requested
+        // at kernel start) covers as much of the context as possible
+        if (a.split_rows > 4 * 32 * KvTile<HD>::NJ)
+            launch_kernel((k_attn_mf<HD, G, 8>), dim3(a.splits, a.nkv, a.batch), dim3(512), 0, st, a);
         else launch_kernel((k_attn_mf<HD, G, 4>), dim3(a.splits, a.nkv, a.batch), dim3(256), 0, st, a);
     } else launch_kernel((k_attn<HD, 0, G>), dim3(a.splits, a.nkv, a.batch), dim3(256), 0, st, a);
     return hipGetLastError();
@@ -809,14 +812,18 @@ hipError_t launch_g(const AttnArgs& a, hipStream_t st) {
 // Context split. Up to 1024 rows a (row, KV head) stays in one workgroup (each wave takes at
 // most two 64-row tiles, cheaper than a merge). Longer contexts are cut into splits of at
 // least 256 rows, as many as it takes to give the chip about two workgroups per CU, at most
-// 128. Splits of 512 rows or more run 8 waves per workgroup, shorter ones 4.
+// 128. Splits of more than 4 tiles run 8 waves per workgroup, shorter ones 4.
 constexpr int ATTN_TARGET_WG = 512;
 constexpr int ATTN_MIN_ROWS = 256;
 void attn_plan(int max_len, int batch, int nkv, int* splits, int* split_rows) {
+    // the bound is rounded up (256, 512, 1024, then multiples of 1024) so that a decode graph
+    // captured for it stays valid while the context grows: rows past a sequence's length cost a
+    // skipped tile or an empty split, a new plan costs a graph capture
     max_len = std::max(max_len, 1);
+    max_len = max_len <= 256 ? 256 : max_len <= 512 ? 512 : (max_len + 1023) / 1024 * 1024;
     if (max_len <= 1024) {
         *splits = 1;
-        *split_rows = (max_len + 63) / 64 * 64;
+        *split_rows = max_len;
         return;
     }
     const int heads = std::max(batch * nkv, 1);

@@ -222,9 +222,18 @@ __device__ int sample_topk(const SampleArgs& a, int b, int slot, int pos, float*
     return s_pick;
 }
 
-__global__ void __launch_bounds__(256) k_sample(const SampleArgs a, const DevWeight t) {
-    __shared__ float sv[4];
-    __shared__ int si[4];
+__device__ __forceinline__ void argmax_take(float& v, int& i, float ov, int oi) {
+    if (ov > v || (ov == v && oi < i)) {
+        v = ov;
+        i = oi;
+    }
+}
+
+constexpr int SAMPLE_THREADS = 1024;
+
+__global__ void __launch_bounds__(SAMPLE_THREADS) k_sample(const SampleArgs a, const DevWeight t) {
+    __shared__ float sv[SAMPLE_THREADS / 64];
+    __shared__ int si[SAMPLE_THREADS / 64];
     __shared__ int s_id;
     __shared__ float sort_v[SORT_N];
     __shared__ int sort_i[SORT_N];
@@ -246,51 +255,87 @@ __global__ void __launch_bounds__(256) k_sample(const SampleArgs a, const DevWei
         embed_stream(t, idx, a.w0, a.x, a.xw, a.ssq, a.ssq_tiles, b);
         return;
     }
+    // Greedy. What does not depend on the chosen id is requested first, in one round of loads:
+    // every tile partial (PT per thread), the entry's slot, step and position, and the next norm
+    // weight of the residual elements this thread writes (EW tiles per wave); the id then costs
+    // one more round (its embedding row, and the penalty count, updated after the barrier).
+    constexpr int PT = 4, EW = 4;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const float* pvb = a.part_val + (int64_t)b * a.tiles;
+    const int32_t* pib = a.part_idx + (int64_t)b * a.tiles;
+    float pv[PT];
+    int pi[PT];
+#pragma unroll
+    for (int k = 0; k < PT; ++k) {
+        const int i = threadIdx.x + k * blockDim.x;
+        pv[k] = i < a.tiles ? pvb[i] : -INFINITY;
+        pi[k] = i < a.tiles ? pib[i] : 0x7fffffff;
+    }
+    int slot = 0, step = 0, pos = 0;
+    if (threadIdx.x == 0) {
+        slot = a.slot[b];
+        pos = a.pos[b];
+        if (a.ids_cap) step = a.step[b];
+    }
+    const int hidden = (int)t.k;
+    float w0v[EW];
+#pragma unroll
+    for (int k = 0; k < EW; ++k) {
+        const int i = (wave + k * nw) * 64 + lane;
+        w0v[k] = i < hidden ? a.w0[i] : 0.f;
+    }
     float v = -INFINITY;
     int idx = 0x7fffffff;
-    for (int i = threadIdx.x; i < a.tiles; i += blockDim.x) {
-        const float ov = a.part_val[(int64_t)b * a.tiles + i];
-        const int oi = a.part_idx[(int64_t)b * a.tiles + i];
-        if (ov > v || (ov == v && oi < idx)) {
-            v = ov;
-            idx = oi;
-        }
-    }
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(v, off);
-        const int oi = __shfl_xor(idx, off);
-        if (ov > v || (ov == v && oi < idx)) {
-            v = ov;
-            idx = oi;
-        }
-    }
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int k = 0; k < PT; ++k) argmax_take(v, idx, pv[k], pi[k]);
+    for (int i = threadIdx.x + PT * blockDim.x; i < a.tiles; i += blockDim.x) argmax_take(v, idx, pvb[i], pib[i]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) argmax_take(v, idx, __shfl_xor(v, off), __shfl_xor(idx, off));
     if (lane == 0) {
         sv[wave] = v;
         si[wave] = idx;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < (int)(blockDim.x >> 6); ++w)
-            if (sv[w] > v || (sv[w] == v && si[w] < idx)) {
-                v = sv[w];
-                idx = si[w];
-            }
+        for (int w = 1; w < nw; ++w) argmax_take(v, idx, sv[w], si[w]);
         if (idx == 0x7fffffff) idx = 0;  // no finite logit: the scan keeps index 0
-        uint16_t* c = a.pen + (int64_t)a.slot[b] * a.vocab + idx;
-        if (*c < 0xFFFF) *c = *c + 1;
         if (a.ids_cap) {
-            const int s = a.step[b];
-            a.ids_cap[(int64_t)s * a.batch + b] = (uint32_t)idx;
-            a.step[b] = s + 1;
+            a.ids_cap[(int64_t)step * a.batch + b] = (uint32_t)idx;
+            a.step[b] = step + 1;
         }
         a.tok[b] = idx;
-        a.pos[b] = a.pos[b] + 1;
+        a.pos[b] = pos + 1;
         s_id = idx;
     }
     __syncthreads();
-    embed_stream(t, s_id, a.w0, a.x, a.xw, a.ssq, a.ssq_tiles, b);
+    const int id = s_id;
+    if (threadIdx.x == 0) {  // penalty count of the chosen id (cpu_engine.rs:2984-2992 counts it)
+        uint16_t* c = a.pen + (int64_t)slot * a.vocab + id;
+        if (*c < 0xFFFF) *c = *c + 1;
+    }
+    // next step's residual stream from the embedding row (embed_stream with the weights loaded)
+    float* xr = a.x + (int64_t)b * hidden;
+    float* xwr = a.xw + (int64_t)b * hidden;
+    auto put = [&](int tl, float w) {
+        const int i = tl * 64 + lane;
+        float e = 0.f;
+        if (i < hidden) {
+            e = embed_elem(t, id, i);
+            xr[i] = e;
+            xwr[i] = e * w;
+        }
+        float sq = e * e;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
+        if (lane == 0) a.ssq[(int64_t)b * a.ssq_tiles + tl] = sq;
+    };
+#pragma unroll
+    for (int k = 0; k < EW; ++k)
+        if (wave + k * nw < a.ssq_tiles) put(wave + k * nw, w0v[k]);
+    for (int tl = wave + EW * nw; tl < a.ssq_tiles; tl += nw) {
+        const int i = tl * 64 + lane;
+        put(tl, i < hidden ? a.w0[i] : 0.f);
+    }
 }
 
 // Cache rows <-> host-layout f32 rows (one thread per element, grid-stride).
@@ -373,7 +418,7 @@ hipError_t launch_sample(const SampleArgs& a, hipStream_t st) {
     if (!a.table || a.ssq_tiles != (int)((a.table->k + 63) / 64) || (a.ids_cap && !a.step)) return hipErrorInvalidValue;
     if (a.temperature > 0.f && (!a.logits || a.top_k < 1 || a.top_k > SAMPLE_TOPK_MAX || a.tiles > SORT_N))
         return hipErrorInvalidValue;
-    launch_kernel(k_sample, dim3(a.batch), dim3(256), 0, st, a, *a.table);
+    launch_kernel(k_sample, dim3(a.batch), dim3(SAMPLE_THREADS), 0, st, a, *a.table);
     return hipGetLastError();
 }
 
