@@ -39,19 +39,58 @@ __device__ __forceinline__ float wave_sum64(float v) {
 }
 
 // rnorm of the residual stream for row b: 1/sqrt(sum_t ssq[b][t] / n + eps), the tiles summed in
-// order (rms_norm_into, cpu_engine.rs:1292-1302, with the sum of squares computed per tile).
+// order (rms_norm_into, cpu_engine.rs:1292-1302, with the sum of squares computed per tile). The
+// tiles are loaded RN_U at a time (index clamped, all in flight) before they are added: a loop of
+// dependent loads here delays the first wave of every consumer kernel by one memory round trip
+// per tile.
+constexpr int RN_U = 16;
+__device__ __forceinline__ float rnorm_sum(const float* s, int n, int i0, float t) {
+    for (; i0 < n; i0 += RN_U) {
+        float v[RN_U];
+#pragma unroll
+        for (int k = 0; k < RN_U; ++k) v[k] = s[min(i0 + k, n - 1)];
+#pragma unroll
+        for (int k = 0; k < RN_U; ++k)
+            if (i0 + k < n) t += v[k];
+    }
+    return t;
+}
 __device__ __forceinline__ float stream_rnorm(const GemvArgs& a, int b) {
-    const float* s = a.ssq_in + (int64_t)b * a.ssq_tiles;
-    float t = 0.f;
-    for (int i = 0; i < a.ssq_tiles; ++i) t += s[i];
+    const float t = rnorm_sum(a.ssq_in + (int64_t)b * a.ssq_tiles, a.ssq_tiles, 0, 0.f);
     return 1.0f / sqrtf(t / a.norm_n + a.eps);
 }
 
-// Per-token RMSNorm factors of a normalized residual-stream input (1 without one), into LDS.
-template <int B>
-__device__ __forceinline__ void load_rnorm(const GemvArgs& a, float* rn) {
-    if (threadIdx.x < B) rn[threadIdx.x] = (a.ssq_in && (int)threadIdx.x < a.batch) ? stream_rnorm(a, threadIdx.x) : 1.0f;
-}
+// The per-token norm factors of a kernel whose activations are a normalized residual stream, in
+// two steps: request() issues the loads of the first NV tiles of token threadIdx.x (< B) early,
+// finish() adds them (and any further tiles) once the kernel's main loop is done and stores the
+// factor (1 without a residual-stream input) to rn[threadIdx.x]. A __syncthreads() must separate
+// finish() from the readers of rn.
+template <int B, int NV = RN_U>
+struct RnormReq {
+    float v[NV];
+    __device__ __forceinline__ bool mine(const GemvArgs& a) const {
+        return a.ssq_in && (int)threadIdx.x < B && (int)threadIdx.x < a.batch;
+    }
+    __device__ __forceinline__ void request(const GemvArgs& a) {
+        if (!mine(a)) return;
+        const float* s = a.ssq_in + (int64_t)threadIdx.x * a.ssq_tiles;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) v[k] = s[min(k, a.ssq_tiles - 1)];
+    }
+    __device__ __forceinline__ void finish(const GemvArgs& a, float* rn) const {
+        if (threadIdx.x >= B) return;
+        if (!mine(a)) {
+            rn[threadIdx.x] = 1.0f;
+            return;
+        }
+        float t = 0.f;
+#pragma unroll
+        for (int k = 0; k < NV; ++k)
+            if (k < a.ssq_tiles) t += v[k];
+        t = rnorm_sum(a.ssq_in + (int64_t)threadIdx.x * a.ssq_tiles, a.ssq_tiles, NV, t);
+        rn[threadIdx.x] = 1.0f / sqrtf(t / a.norm_n + a.eps);
+    }
+};
 
 // K split over workgroups (a.ksw > 1): publish this split's TOT sums and let the tile's last
 // workgroup add all splits in split order; returns false in every other workgroup, which then

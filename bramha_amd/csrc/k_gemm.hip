@@ -5,8 +5,9 @@
 // 3325-3339) and, per token, matvec_mul_into (:1307-1444): Y[b][n] = sum_k W[n][k] X[b][k].
 //
 // Design: a workgroup owns a tile of 64 * RW weight rows and a K range; K splits further over
-// the workgroup's 4 wavefronts per 64-row group (combined in LDS in a fixed order) and, for
-// matrices with few row tiles, over workgroups (the ordered split reduction of k_epilogue.h).
+// the workgroup's KW wavefronts per 64-row group (their sums meet in an LDS tree, halving in a
+// fixed order) and, for matrices with few row tiles, over workgroups (the ordered split
+// reduction of k_epilogue.h).
 // Each wavefront runs v_mfma_f32_16x16x32_f16 over its 64 rows as four 16-row A blocks — one
 // dword of 8 nibbles per lane per block, decoded to exact fp16 (q - 8) — with the tokens as the
 // B operand: f32 activations split into fp16 hi + lo (hi + lo carries ~22 bits), so each product
@@ -31,27 +32,28 @@ struct MfStage {
     uint4 x[S][TB][2];       // f32 activations of token tb * 16 + lr, k = 8 lg .. + 7
 };
 
-template <int FMT, int B, int EPI, int RW>
-__global__ void __launch_bounds__(256 * RW) k_gemm_mf(const GemvArgs a) {
+template <int FMT, int B, int EPI, int RW, int KW, int S>
+__global__ void __launch_bounds__(64 * KW * RW) k_gemm_mf(const GemvArgs a) {
     constexpr int NACC = EPI == EPI_SILU ? 2 : 1;
     constexpr int ROWS = 64 * RW;
     constexpr int TB = B / 16;
     constexpr int TOT = NACC * B * ROWS;
-    constexpr int S = 1;  // chunks per pipeline stage (two stages in flight; more costs occupancy)
+    // S: chunks per pipeline stage (two stages in flight)
     extern __shared__ float smem[];
     float* rn = smem;          // [32] per-token norm factors
     float* comb = smem + 32;   // [NACC][B][ROWS] sums, then epilogue scratch [B][ROWS]
+    float* tree = comb + TOT;  // [KW / 2][B][ROWS] wave-sum exchange (before the epilogue)
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lr = lane & 15, lg = lane >> 4;
-    const int rw = wave % RW, kw = wave / RW;  // 64-row group, K-split index (0..3)
+    const int rw = wave % RW, kw = wave / RW;  // 64-row group, K-split index (0 .. KW - 1)
     const int ksw = a.ksw;
     const int tiles = gridDim.x / ksw;
     const int tile = blockIdx.x % tiles, kws = blockIdx.x / tiles;
     const int per_wg = (a.C + ksw - 1) / ksw;
     const int wc0 = kws * per_wg, wc1 = min(a.C, wc0 + per_wg);
-    const int per = (max(wc1 - wc0, 0) + 3) / 4;
+    const int per = (max(wc1 - wc0, 0) + KW - 1) / KW;
     const int c0 = wc0 + kw * per, c1 = min(wc1, c0 + per);
 
     // the group's 64 rows; a group past the padded matrix re-reads the last one (never stored)
@@ -139,7 +141,8 @@ __global__ void __launch_bounds__(256 * RW) k_gemm_mf(const GemvArgs a) {
 
     MfStage<NACC, TB, S> s0, s1;
     if (c0 < c1) fetch(c0, s0);
-    load_rnorm<B>(a, rn);
+    RnormReq<B> rq;
+    rq.request(a);
     if (c0 < c1) {
         for (int c = c0;; c += 2 * S) {
             fetch(c + S, s1);
@@ -151,39 +154,65 @@ __global__ void __launch_bounds__(256 * RW) k_gemm_mf(const GemvArgs a) {
         }
     }
 
-    // D layout: lane holds token tb * 16 + lr, rows 4 * lg + v of each 16-row block. The four
-    // K-split waves of a row group add into one buffer in turn (a fixed order).
+    // D layout: lane holds token tb * 16 + lr, rows 4 * lg + v of each 16-row block. The K-split
+    // waves of a row group halve in rounds: waves [h, 2h) hand their sums to waves [0, h) through
+    // LDS; wave 0 ends with the group's total.
     constexpr float FIN = FMT == BH_Q4_ROW ? 16.0f : 1.0f;  // row formats: the epilogue scales by s/16
+    rq.finish(a, rn);  // read by the epilogue, after the barriers below
+    auto at = [&](int rb, int tb, int v) { return (tb * 16 + lr) * ROWS + rw * 64 + rb * 16 + 4 * lg + v; };
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        if (kw == w) {
+    for (int j = 0; j < NACC; ++j) {
 #pragma unroll
-            for (int j = 0; j < NACC; ++j)
+        for (int h = KW / 2; h >= 1; h >>= 1) {
+            if (kw >= h && kw < 2 * h) {
+                float* buf = tree + (kw - h) * B * ROWS;
 #pragma unroll
                 for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
                     for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
-                        for (int v = 0; v < 4; ++v) {
-                            float* d = &comb[(j * B + tb * 16 + lr) * ROWS + rw * 64 + rb * 16 + 4 * lg + v];
-                            *d = (w == 0 ? 0.f : *d) + acc[j][rb][tb][v] * FIN;
-                        }
+                        for (int v = 0; v < 4; ++v) buf[at(rb, tb, v)] = acc[j][rb][tb][v];
+            }
+            __syncthreads();
+            if (kw < h) {
+                const float* buf = tree + kw * B * ROWS;
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                    for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) acc[j][rb][tb][v] += buf[at(rb, tb, v)];
+            }
+            __syncthreads();
         }
-        __syncthreads();
+        if (kw == 0) {
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) comb[j * B * ROWS + at(rb, tb, v)] = acc[j][rb][tb][v] * FIN;
+        }
     }
+    __syncthreads();
     if (ksw > 1 && !split_reduce<TOT>(a, comb, tile, kws)) return;
     __syncthreads();
     run_epilogue<FMT, B, EPI, ROWS>(a, comb, comb + TOT, rn, (int64_t)tile * ROWS);
 }
 
+// Waves per row group and chunks per stage: 4 and 1. Measured at 16 and 32 tokens on the
+// Qwen2-0.5B shapes, 8 waves or two-chunk stages are 1-3 us slower per pass (896 x 896 at 32
+// tokens: 12.8 us; 8 waves 15.8; two-chunk stages 13.7) and halve the LM head's rate.
 template <int FMT, int B, int EPI, int RW>
 hipError_t launch_t(const GemvArgs& a, hipStream_t st) {
     constexpr int NACC = EPI == EPI_SILU ? 2 : 1;
     constexpr int ROWS = 64 * RW;
+    constexpr int KW = 4;
+    constexpr int S = 1;
     const int tiles = (a.n_pad + ROWS - 1) / ROWS;
-    const size_t shm = (32 + (size_t)NACC * B * ROWS + (size_t)B * ROWS) * sizeof(float);
+    const size_t shm = (32 + (size_t)NACC * B * ROWS + (size_t)std::max(1, KW / 2) * B * ROWS) * sizeof(float);
     if (shm > 64 * 1024) return hipErrorInvalidValue;
-    launch_kernel((k_gemm_mf<FMT, B, EPI, RW>), dim3(tiles * a.ksw), dim3(256 * RW), shm, st, a);
+    launch_kernel((k_gemm_mf<FMT, B, EPI, RW, KW, S>), dim3(tiles * a.ksw), dim3(64 * KW * RW), shm, st, a);
     return hipGetLastError();
 }
 

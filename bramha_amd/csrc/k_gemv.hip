@@ -58,11 +58,12 @@ __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
     {
         float acc[NACC][B];
         float touch = 0.f;
+        RnormReq<B, B == 1 ? RN_U : 8> rq;  // fewer early tiles where registers are tight
         stream_chunks<FMT, B, NACC, U, CP>(a, nl, c0, c1, acc, [&] {
             // the activation touch (bs1 decode step: 1232 -> 1291 tok/s), the norm factors and the
             // batch-1 epilogue operands load while the first weight stage is in flight
             touch = touch_activations<B, E>(a, wc0, wc1);
-            load_rnorm<B>(a, rn);
+            rq.request(a);
             if constexpr (B == 1)
                 if (threadIdx.x < ROWS) pre.load(a, (int64_t)tile * ROWS);
         });
@@ -70,6 +71,7 @@ __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
         for (int j = 0; j < NACC; ++j)
 #pragma unroll
             for (int b = 0; b < B; ++b) comb[kw * TOT + (j * B + b) * ROWS + r] = acc[j][b];
+        rq.finish(a, rn);
         asm volatile("" ::"v"(touch));
     }
 
