@@ -42,7 +42,7 @@ __global__ void __launch_bounds__(64 * KW * RW) k_gemm_mf(const GemvArgs a) {
     extern __shared__ float smem[];
     float* rn = smem;          // [32] per-token norm factors
     float* comb = smem + 32;   // [NACC][B][ROWS] sums, then epilogue scratch [B][ROWS]
-    float* tree = comb + TOT;  // [KW / 2][B][ROWS] wave-sum exchange (before the epilogue)
+    float* tree = comb + TOT;  // [KW / 2][B][ROWS + 4] wave-sum exchange (before the epilogue)
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -154,18 +154,23 @@ __global__ void __launch_bounds__(64 * KW * RW) k_gemm_mf(const GemvArgs a) {
         }
     }
 
+    rq.finish(a, rn);  // read by the epilogue, after the barriers below
     // D layout: lane holds token tb * 16 + lr, rows 4 * lg + v of each 16-row block. The K-split
     // waves of a row group halve in rounds: waves [h, 2h) hand their sums to waves [0, h) through
-    // LDS; wave 0 ends with the group's total.
+    // LDS; wave 0 ends with the group's total. In the exchange buffers a token's rows are TS =
+    // ROWS + 4 floats apart and row 4 lg + v of a block sits at 4 v + lg, so the 64 lanes of one
+    // D element fall in 64 distinct banks (4 lr + lg); with rows in natural order at stride ROWS
+    // the 16 lr lanes shared a bank (16-way conflicts: 94K conflict cycles of 420K busy on
+    // 896 x 896 at 32 tokens). The totals are copied to comb's [j][b][row] order at the end.
     constexpr float FIN = FMT == BH_Q4_ROW ? 16.0f : 1.0f;  // row formats: the epilogue scales by s/16
-    rq.finish(a, rn);  // read by the epilogue, after the barriers below
-    auto at = [&](int rb, int tb, int v) { return (tb * 16 + lr) * ROWS + rw * 64 + rb * 16 + 4 * lg + v; };
+    constexpr int TS = ROWS + 4;
+    auto at = [&](int rb, int tb, int v) { return (tb * 16 + lr) * TS + rw * 64 + rb * 16 + 4 * v + lg; };
 #pragma unroll
     for (int j = 0; j < NACC; ++j) {
 #pragma unroll
         for (int h = KW / 2; h >= 1; h >>= 1) {
             if (kw >= h && kw < 2 * h) {
-                float* buf = tree + (kw - h) * B * ROWS;
+                float* buf = tree + (kw - h) * B * TS;
 #pragma unroll
                 for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
@@ -175,7 +180,7 @@ __global__ void __launch_bounds__(64 * KW * RW) k_gemm_mf(const GemvArgs a) {
             }
             __syncthreads();
             if (kw < h) {
-                const float* buf = tree + kw * B * ROWS;
+                const float* buf = tree + kw * B * TS;
 #pragma unroll
                 for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
@@ -191,29 +196,41 @@ __global__ void __launch_bounds__(64 * KW * RW) k_gemm_mf(const GemvArgs a) {
 #pragma unroll
                 for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) comb[j * B * ROWS + at(rb, tb, v)] = acc[j][rb][tb][v] * FIN;
+                    for (int v = 0; v < 4; ++v) tree[at(rb, tb, v)] = acc[j][rb][tb][v] * FIN;
         }
+        __syncthreads();
+        // to [b][row]: row r of a 16-row block is at (r & 3) * 4 + (r >> 2) & 3
+        for (int i = threadIdx.x; i < B * ROWS; i += blockDim.x) {
+            const int b = i / ROWS, r = i % ROWS;
+            comb[j * B * ROWS + i] = tree[b * TS + (r & ~15) + ((r & 3) << 2) + ((r >> 2) & 3)];
+        }
+        __syncthreads();
     }
-    __syncthreads();
     if (ksw > 1 && !split_reduce<TOT>(a, comb, tile, kws)) return;
     __syncthreads();
     run_epilogue<FMT, B, EPI, ROWS>(a, comb, comb + TOT, rn, (int64_t)tile * ROWS);
 }
 
-// Waves per row group and chunks per stage: 4 and 1. Measured at 16 and 32 tokens on the
-// Qwen2-0.5B shapes, 8 waves or two-chunk stages are 1-3 us slower per pass (896 x 896 at 32
-// tokens: 12.8 us; 8 waves 15.8; two-chunk stages 13.7) and halve the LM head's rate.
-template <int FMT, int B, int EPI, int RW>
-hipError_t launch_t(const GemvArgs& a, hipStream_t st) {
+// Waves per row group: 8 for passes of at most 512 workgroups, whose time is the chain of loads
+// each wave walks (896 x 4864 at 32 tokens: 17.7 -> 13.8 us; 896-wide K unchanged), 4 for larger
+// ones, where occupancy decides (the 151936-row LM head at 32 tokens: 66 us with 4, 103 with 8).
+// One chunk per stage: two-chunk stages measured slower at every shape.
+template <int FMT, int B, int EPI, int RW, int KW>
+hipError_t launch_k(const GemvArgs& a, hipStream_t st) {
     constexpr int NACC = EPI == EPI_SILU ? 2 : 1;
     constexpr int ROWS = 64 * RW;
-    constexpr int KW = 4;
-    constexpr int S = 1;
     const int tiles = (a.n_pad + ROWS - 1) / ROWS;
-    const size_t shm = (32 + (size_t)NACC * B * ROWS + (size_t)std::max(1, KW / 2) * B * ROWS) * sizeof(float);
+    const size_t shm = (32 + (size_t)NACC * B * ROWS + (size_t)std::max(1, KW / 2) * B * (ROWS + 4)) * sizeof(float);
     if (shm > 64 * 1024) return hipErrorInvalidValue;
-    launch_kernel((k_gemm_mf<FMT, B, EPI, RW, KW, S>), dim3(tiles * a.ksw), dim3(64 * KW * RW), shm, st, a);
+    launch_kernel((k_gemm_mf<FMT, B, EPI, RW, KW, 1>), dim3(tiles * a.ksw), dim3(64 * KW * RW), shm, st, a);
     return hipGetLastError();
+}
+
+template <int FMT, int B, int EPI, int RW>
+hipError_t launch_t(const GemvArgs& a, hipStream_t st) {
+    if constexpr (RW == 1)
+        if ((a.n_pad + 63) / 64 * a.ksw <= 512) return launch_k<FMT, B, EPI, RW, 8>(a, st);
+    return launch_k<FMT, B, EPI, RW, 4>(a, st);
 }
 
 template <int FMT, int EPI, int RW>
