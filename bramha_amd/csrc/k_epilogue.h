@@ -128,6 +128,77 @@ __device__ __forceinline__ bool split_reduce(const GemvArgs& a, float* comb, int
     return true;
 }
 
+// LM-head element of token b, row nn: the raw logit is stored, then the repetition penalty
+// (cpu_engine.rs:2984-2992) applied `cnt` times; -inf for rows past the vocabulary, tokens past
+// the batch and NaN (the first-max scan uses `>`, so NaN never wins).
+template <int FMT>
+__device__ __forceinline__ float lm_elem(const GemvArgs& a, float f, int b, int64_t nn, const float* rn, int cnt) {
+    if (nn >= a.N || b >= a.batch) return -INFINITY;
+    float v = f * row_scale<FMT>(a.S, nn) * rn[b];
+    a.y[(int64_t)b * a.ldy + nn] = v;
+    for (int t = 0; t < cnt; ++t) v = v > 0.f ? v / 1.15f : v * 1.15f;
+    return v > -INFINITY ? v : -INFINITY;
+}
+
+// One argmax per token and 64-row sub-tile of scratch [B][ROWS] (partials stay indexed by
+// 64-row tiles); ties keep the lower index.
+template <int B, int ROWS>
+__device__ __forceinline__ void lm_argmax(const GemvArgs& a, const float* scratch, int64_t row0) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    constexpr int SUB = ROWS / 64;
+    const int tiles64 = (int)((a.n_pad + 63) / 64);
+    for (int q = wave; q < B * SUB; q += nwaves) {
+        const int b = q / SUB, sub = q % SUB;
+        if (b >= a.batch) continue;
+        float v = scratch[b * ROWS + sub * 64 + lane];
+        int idx = v > -INFINITY ? (int)(row0 + sub * 64 + lane) : 0x7fffffff;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(v, off);
+            const int oi = __shfl_xor(idx, off);
+            argmax_combine(v, idx, ov, oi);
+        }
+        const int64_t t64 = row0 / 64 + sub;
+        if (lane == 0 && t64 < tiles64) {
+            a.part_val[(int64_t)b * tiles64 + t64] = v;
+            a.part_idx[(int64_t)b * tiles64 + t64] = idx;
+        }
+    }
+}
+
+// Penalty counts of the LM-head epilogue of a workgroup of NT threads, requested at kernel start:
+// element i = threadIdx.x + k NT of the [B][ROWS] tile at row0. ROWS is a multiple of 64, so a
+// wave's elements share their token and its slot arrives through a scalar load; only the count
+// loads themselves are vector loads, issued without waiting on the weight stream.
+template <int B, int ROWS, int NT>
+struct PenPre {
+    static constexpr int PER = (B * ROWS + NT - 1) / NT;
+    uint32_t c[PER];
+    __device__ __forceinline__ void load(const GemvArgs& a, int64_t row0) {
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int i = threadIdx.x + k * NT;
+            const int b = __builtin_amdgcn_readfirstlane((int)((threadIdx.x + k * NT) / ROWS));
+            const int64_t nn = row0 + i % ROWS;
+            c[k] = 0;
+            if (i < B * ROWS && b < a.batch && nn < a.N) c[k] = a.pen[(int64_t)a.slot[b] * a.vocab + nn];
+        }
+    }
+};
+
+// The batched LM-head epilogue with the counts of PenPre (run_epilogue's EPI_LMHEAD otherwise).
+template <int FMT, int B, int ROWS, int NT>
+__device__ __forceinline__ void run_lmhead_pre(const GemvArgs& a, const float* fin, float* scratch, const float* rn,
+                                               int64_t row0, const PenPre<B, ROWS, NT>& pp) {
+#pragma unroll
+    for (int k = 0; k < PenPre<B, ROWS, NT>::PER; ++k) {
+        const int i = threadIdx.x + k * NT;
+        if (i < B * ROWS) scratch[i] = lm_elem<FMT>(a, fin[i], i / ROWS, row0 + i % ROWS, rn, (int)pp.c[k]);
+    }
+    __syncthreads();
+    lm_argmax<B, ROWS>(a, scratch, row0);
+}
+
 // Epilogue operands of a batch-1 launch for the weight row row0 + threadIdx.x (threadIdx.x <
 // ROWS: the thread that finishes that row), loaded at the start of the kernel so that their
 // latency — including the position -> RoPE table and slot -> penalty chains — hides under the
@@ -225,32 +296,9 @@ __device__ __forceinline__ void run_epilogue(const GemvArgs& a, const float* fin
                     }
                 }
             } else if constexpr (EPI == EPI_LMHEAD) {
-                float pv = -INFINITY;
-                if (ok) {
-                    float v = fin[rr] * row_scale<FMT>(a.S, nn) * rn[0];
-                    a.y[nn] = v;
-                    for (int t = 0; t < pre->cnt; ++t) v = v > 0.f ? v / 1.15f : v * 1.15f;
-                    pv = v > -INFINITY ? v : -INFINITY;
-                }
-                if (rr < ROWS) scratch[rr] = pv;
+                if (rr < ROWS) scratch[rr] = lm_elem<FMT>(a, fin[rr], 0, nn, rn, pre->cnt);
                 __syncthreads();
-                constexpr int SUB = ROWS / 64;
-                const int tiles64 = (int)((a.n_pad + 63) / 64);
-                for (int q = wave; q < SUB; q += nwaves) {
-                    float v = scratch[q * 64 + lane];
-                    int idx = v > -INFINITY ? (int)(row0 + q * 64 + lane) : 0x7fffffff;
-#pragma unroll
-                    for (int off = 32; off > 0; off >>= 1) {
-                        const float ov = __shfl_xor(v, off);
-                        const int oi = __shfl_xor(idx, off);
-                        argmax_combine(v, idx, ov, oi);
-                    }
-                    const int64_t t64 = row0 / 64 + q;
-                    if (lane == 0 && t64 < tiles64) {
-                        a.part_val[t64] = v;
-                        a.part_idx[t64] = idx;
-                    }
-                }
+                lm_argmax<1, ROWS>(a, scratch, row0);
             }
             return;
         }
@@ -335,41 +383,15 @@ __device__ __forceinline__ void run_epilogue(const GemvArgs& a, const float* fin
             }
         }
     } else if constexpr (EPI == EPI_LMHEAD) {
-        // raw logits out, then repetition penalty (cpu_engine.rs:2984-2992) in LDS
+        // raw logits out, then the repetition penalty, in LDS; then the per-tile argmax
         for (int i = threadIdx.x; i < B * ROWS; i += blockDim.x) {
-            const int b = i / ROWS, rr = i % ROWS;
-            const int64_t nn = row0 + rr;
-            float pv = -INFINITY;
-            if (nn < a.N && b < a.batch) {
-                float v = fin[i] * row_scale<FMT>(a.S, nn) * rn[b];
-                a.y[(int64_t)b * a.ldy + nn] = v;
-                const int cnt = a.pen[(int64_t)a.slot[b] * a.vocab + nn];
-                for (int t = 0; t < cnt; ++t) v = v > 0.f ? v / 1.15f : v * 1.15f;
-                pv = v > -INFINITY ? v : -INFINITY;  // NaN never wins (first-max scan uses `>`)
-            }
-            scratch[i] = pv;
+            const int b = i / ROWS;
+            const int64_t nn = row0 + i % ROWS;
+            const int cnt = (nn < a.N && b < a.batch) ? a.pen[(int64_t)a.slot[b] * a.vocab + nn] : 0;
+            scratch[i] = lm_elem<FMT>(a, fin[i], b, nn, rn, cnt);
         }
         __syncthreads();
-        // one argmax per 64-row sub-tile: partials stay indexed by 64-row tiles
-        constexpr int SUB = ROWS / 64;
-        const int tiles64 = (int)((a.n_pad + 63) / 64);
-        for (int q = wave; q < B * SUB; q += nwaves) {
-            const int b = q / SUB, sub = q % SUB;
-            if (b >= a.batch) continue;
-            float v = scratch[b * ROWS + sub * 64 + lane];
-            int idx = v > -INFINITY ? (int)(row0 + sub * 64 + lane) : 0x7fffffff;
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) {
-                const float ov = __shfl_xor(v, off);
-                const int oi = __shfl_xor(idx, off);
-                argmax_combine(v, idx, ov, oi);
-            }
-            const int64_t t64 = row0 / 64 + sub;
-            if (lane == 0 && t64 < tiles64) {
-                a.part_val[(int64_t)b * tiles64 + t64] = v;
-                a.part_idx[(int64_t)b * tiles64 + t64] = idx;
-            }
-        }
+        lm_argmax<B, ROWS>(a, scratch, row0);
     }
 }
 

@@ -143,6 +143,9 @@ __global__ void __launch_bounds__(64 * KW * RW) k_gemm_mf(const GemvArgs a) {
     if (c0 < c1) fetch(c0, s0);
     RnormReq<B> rq;
     rq.request(a);
+    constexpr int NT = 64 * KW * RW;
+    PenPre<B, ROWS, NT> pp;  // LM head: penalty counts, in flight with the weight stream
+    if constexpr (EPI == EPI_LMHEAD) pp.load(a, (int64_t)tile * ROWS);
     if (c0 < c1) {
         for (int c = c0;; c += 2 * S) {
             fetch(c + S, s1);
@@ -208,7 +211,10 @@ __global__ void __launch_bounds__(64 * KW * RW) k_gemm_mf(const GemvArgs a) {
     }
     if (ksw > 1 && !split_reduce<TOT>(a, comb, tile, kws)) return;
     __syncthreads();
-    run_epilogue<FMT, B, EPI, ROWS>(a, comb, comb + TOT, rn, (int64_t)tile * ROWS);
+    if constexpr (EPI == EPI_LMHEAD)
+        run_lmhead_pre<FMT, B, ROWS, NT>(a, comb, comb + TOT, rn, (int64_t)tile * ROWS, pp);
+    else
+        run_epilogue<FMT, B, EPI, ROWS>(a, comb, comb + TOT, rn, (int64_t)tile * ROWS);
 }
 
 // Waves per row group: 8 for passes of at most 512 workgroups, whose time is the chain of loads
