@@ -329,6 +329,8 @@ def main():
     ap.add_argument("--prompt", type=int, default=32)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-bs1", action="store_true")
+    ap.add_argument("--only-bs32", action="store_true",
+                    help="for kernel traces: only the batch-32 decode, printed as its own JSON object")
     ap.add_argument("--no-sweeps", action="store_true", help="skip the isolated GEMV and attention sweeps")
     ap.add_argument("--full", action="store_true",
                     help="also run the ragged 32-sequence decode and the Qwen2-7B prefill + decode workloads")
@@ -371,6 +373,15 @@ def main():
         plane.close()
         return
     total = args.warmup + args.steps
+    if args.only_bs32:
+        m32, _ = build_model(plane, 32, args.prompt, total + 32)
+        dt32 = timed_decode(m32, args.steps, args.warmup)
+        kern32, roof32 = roofline(m32)
+        print(json.dumps({"bs32": {"value": 32 * args.steps / dt32, "unit": "tok/s",
+                                   "ms_per_step": dt32 * 1e3 / args.steps, "roofline": roof32}}), flush=True)
+        m32.close()
+        plane.close()
+        return
     log("building bs1 model")
     m1, cfg = build_model(plane, 1, args.prompt, total + 32)
     dt1 = timed_decode(m1, args.steps, args.warmup)
