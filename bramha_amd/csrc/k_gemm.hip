@@ -151,7 +151,9 @@ __global__ void __launch_bounds__(64 * KW * RW) k_gemm_mf(const GemvArgs a) {
             fetch(c + S, s1);
             consume(c, s0);
             if (c + S >= c1) break;
-            fetch(c + 2 * S, s0);
+            // the 8-wave (latency-bound) launches skip the clamped re-read past their last chunk:
+            // 896 x 896 at 32 tokens 11.1 -> 10.1 us; the 4-wave LM head is faster with it
+            if (KW == 4 || c + 2 * S < c1) fetch(c + 2 * S, s0);
             consume(c + S, s1);
             if (c + 2 * S >= c1) break;
         }
