@@ -89,6 +89,25 @@ def test_batch20_decode_mfma(plane):
         assert np.max(np.abs(lg[:n, s] - wl)) <= 1e-4 * max(1.0, np.abs(wl).max()), s
 
 
+@pytest.mark.parametrize("nseq", [16, 32])
+def test_batch_decode_large_vocab(plane, nseq):
+    # a 40000-id vocabulary: the LM head's MFMA pass has 626 row tiles (the 4-wave variant that
+    # requests the penalty counts at kernel start), every step's ids and logits as the oracle's
+    cfg = tiny_cfg(Q4_G32, Q4_G32, max_seqs=nseq, kv_rows=nseq * 64, vocab=40000)
+    om, gm = _pair(plane, cfg, seed=29)
+    prompts = [prompt(3 + (s * 5) % 20, cfg.vocab, seed=200 + s) for s in range(nseq)]
+    for s, p in enumerate(prompts):
+        gm.seq_open(s, 64)
+        gm.prefill(s, p[:-1])
+    gm.decode_setup(list(range(nseq)), [p[-1] for p in prompts])
+    ids, lg = gm.decode(6, want_logits=True)
+    for s, p in enumerate(prompts):
+        want, wl = om.generate(p, 6, want_logits=True)
+        n = len(want)
+        assert np.array_equal(ids[:n, s], want), s
+        assert np.max(np.abs(lg[:n, s] - wl)) <= 1e-4 * max(1.0, np.abs(wl).max()), s
+
+
 def test_tiny_sink_eviction(plane):
     cfg = tiny_cfg(F32, F32, max_context=16, sink_tokens=4)
     om, gm = _pair(plane, cfg, seed=5)
