@@ -134,6 +134,9 @@ struct GemvArgs {
     int vocab = 0;
     float* part_val = nullptr;         // [batch][tiles64]
     int32_t* part_idx = nullptr;
+    // prefill passes (launch_gemm_pf): scratch of batch * C * 64 fp16 for the activations split
+    // once into hi + lo (k_prefill.hip); null: every workgroup splits them itself
+    uint16_t* xhl = nullptr;
 };
 
 // The arguments of tokens b0 .. b0 + n - 1 of `a`: every per-token pointer advanced by b0.

@@ -67,6 +67,7 @@ struct bh_model {
     int32_t* attn_cnt = nullptr;   // [max_tokens][n_kv] split-merge counters
     size_t attn_rows = 0;          // query rows of attn_part
     float* split_part = nullptr;   // K-split sums of split projections
+    uint16_t* xhl = nullptr;       // prefill passes: activations split into fp16 hi + lo
     int32_t* split_cnt = nullptr;  // their per-tile arrival counters (zero when idle)
     // decode batch state (read by the captured graph) and prefill staging, kept apart so a
     // prefill between decode calls leaves the batch intact
@@ -181,6 +182,7 @@ void weight_args(bh_model* m, GemvArgs& a, const DevWeight& w) {
     a.ksw = 0;
     a.part = m->split_part;
     a.tile_cnt = m->split_cnt;
+    a.xhl = m->xhl;
 }
 
 // One forward pass over M tokens whose residual stream (x, xw, ssq) holds their embedding rows:
@@ -485,6 +487,10 @@ int bh_model_create(bh_ctx* ctx, const bh_model_config* cfg, bh_model** out) {
     };
     for (auto& b : bufs)
         if ((e = dmalloc(m, b.p, b.bytes)) != hipSuccess) return bail(e, "hipMalloc(activations)");
+    if (T >= (size_t)PF_MIN_TOKENS) {  // passes that reach the tiled prefill GEMM
+        const size_t kmax = std::max<size_t>({(size_t)c.hidden, (size_t)QD, (size_t)c.ffn});
+        if ((e = dmalloc(m, (void**)&m->xhl, T * kmax * 4)) != hipSuccess) return bail(e, "hipMalloc(activation split)");
+    }
     e = hipHostMalloc(&m->h_stage, (4 * T + 16) * 8, hipHostMallocDefault);
     if (e != hipSuccess) {
         m->h_stage = nullptr;

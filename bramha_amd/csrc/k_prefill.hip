@@ -33,10 +33,28 @@ template <int NACC, int TBW>
 struct PfStage {
     uint32_t w[NACC][4];  // [matrix][row block]: dword lg of row rb * 16 + lr
     uint2 s[NACC][4];     // fp16 group scales of rows rb * 16 + 4 lg .. + 3
-    uint4 x[TBW][2];      // f32 activations of token tb * 16 + lr, k = 8 lg .. + 7
+    uint4 x[TBW][2];      // token tb * 16 + lr, k = 8 lg .. + 7: f32, or (PRE) fp16 hi and lo
 };
 
-template <int FMT, int EPI>
+// The activations of a prefill pass split once into the MFMA B operands: for token m and chunk c,
+// 64 fp16 at (m * C + c) * 64: hi of k = 8 lg + kperm(s) at 8 lg + s, lo at 32 + 8 lg + s (split8,
+// the values every workgroup would compute). One thread per 8 elements.
+__global__ void __launch_bounds__(256) k_split_act(const float* __restrict__ x, int64_t ldx, int M, int C,
+                                                   uint16_t* __restrict__ xhl) {
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // (m, c, lg)
+    if (g >= (int64_t)M * C * 4) return;
+    const int lg = (int)(g & 3);
+    const int64_t mc = g >> 2;
+    const int64_t m = mc / C, c = mc % C;
+    const float4* src = (const float4*)(x + m * ldx + c * 32 + lg * 8);
+    half8 hi, lo;
+    split8(src[0], src[1], hi, lo);
+    uint4* dst = (uint4*)(xhl + mc * 64 + lg * 8);
+    dst[0] = __builtin_bit_cast(uint4, hi);
+    dst[4] = __builtin_bit_cast(uint4, lo);
+}
+
+template <int FMT, int EPI, bool PRE>
 __global__ void __launch_bounds__(256) k_gemm_pf(const GemvArgs a) {
     constexpr int NACC = EPI == EPI_SILU ? 2 : 1;
     constexpr int TBW = NACC == 2 ? 2 : 4;  // 16-token blocks per wavefront
@@ -66,12 +84,17 @@ __global__ void __launch_bounds__(256) k_gemm_pf(const GemvArgs a) {
         if constexpr (NACC == 2)
             rS[1] = __builtin_amdgcn_make_buffer_rsrc((void*)a.S2, (short)0, a.C * a.n_pad * 2, 0x00020000);
     }
-    const __amdgpu_buffer_rsrc_t rX = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)a.x, (short)0, (int)((int64_t)a.batch * a.ldx * 4), 0x00020000);
+    // f32 rows of ldx floats, or (PRE) rows of C * 64 fp16; either way 128 bytes per chunk
+    const __amdgpu_buffer_rsrc_t rX =
+        PRE ? __builtin_amdgcn_make_buffer_rsrc((void*)a.xhl, (short)0, (int)((int64_t)a.batch * a.C * 128), 0x00020000)
+            : __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)((int64_t)a.batch * a.ldx * 4), 0x00020000);
     // token of block tb for this lane, clamped into the chunk (rows past it are never stored)
     int vo_x[TBW];
 #pragma unroll
-    for (int tb = 0; tb < TBW; ++tb) vo_x[tb] = (min(wtok0 + tb * 16 + lr, a.batch - 1) * (int)a.ldx + 8 * lg) * 4;
+    for (int tb = 0; tb < TBW; ++tb) {
+        const int tok = min(wtok0 + tb * 16 + lr, a.batch - 1);
+        vo_x[tb] = PRE ? tok * a.C * 128 + 16 * lg : (tok * (int)a.ldx + 8 * lg) * 4;
+    }
 
     auto fetch = [&](int c, PfStage<NACC, TBW>& st) {
         const int cc = min(c, a.C - 1);
@@ -88,8 +111,9 @@ __global__ void __launch_bounds__(256) k_gemm_pf(const GemvArgs a) {
 #pragma unroll
         for (int tb = 0; tb < TBW; ++tb)
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
-                st.x[tb][h] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rX, vo_x[tb] + h * 16, cc * 128, 0));
+            for (int h = 0; h < 2; ++h)  // f32: the two halves of 8 values; PRE: hi at +0, lo at +64 bytes
+                st.x[tb][h] = __builtin_bit_cast(
+                    uint4, __builtin_amdgcn_raw_buffer_load_b128(rX, vo_x[tb] + h * (PRE ? 64 : 16), cc * 128, 0));
     };
 
     f32x4 acc[NACC][4][TBW];
@@ -103,8 +127,14 @@ __global__ void __launch_bounds__(256) k_gemm_pf(const GemvArgs a) {
     auto consume = [&](const PfStage<NACC, TBW>& st) {
         half8 bh[TBW], bl[TBW];
 #pragma unroll
-        for (int tb = 0; tb < TBW; ++tb)
-            split8(__builtin_bit_cast(float4, st.x[tb][0]), __builtin_bit_cast(float4, st.x[tb][1]), bh[tb], bl[tb]);
+        for (int tb = 0; tb < TBW; ++tb) {
+            if constexpr (PRE) {
+                bh[tb] = __builtin_bit_cast(half8, st.x[tb][0]);
+                bl[tb] = __builtin_bit_cast(half8, st.x[tb][1]);
+            } else {
+                split8(__builtin_bit_cast(float4, st.x[tb][0]), __builtin_bit_cast(float4, st.x[tb][1]), bh[tb], bl[tb]);
+            }
+        }
 #pragma unroll
         for (int j = 0; j < NACC; ++j)
 #pragma unroll
@@ -179,7 +209,16 @@ hipError_t launch_t(const GemvArgs& a, hipStream_t st) {
     constexpr int MT = NACC == 2 ? 64 : 128;
     const int mtiles = (a.batch + MT - 1) / MT;
     const int ntiles = (a.n_pad + PF_ROWS - 1) / PF_ROWS;
-    launch_kernel((k_gemm_pf<FMT, EPI>), dim3(mtiles * ntiles), dim3(256), 0, st, a);
+    if (a.xhl) {
+        // split the activations once (the VALU work of the in-kernel split, ~half of the inner
+        // loop's, is otherwise repeated by every row tile)
+        const int64_t groups = (int64_t)a.batch * a.C * 4;
+        launch_kernel(k_split_act, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, st, a.x, a.ldx, a.batch, a.C,
+                      a.xhl);
+        launch_kernel((k_gemm_pf<FMT, EPI, true>), dim3(mtiles * ntiles), dim3(256), 0, st, a);
+    } else {
+        launch_kernel((k_gemm_pf<FMT, EPI, false>), dim3(mtiles * ntiles), dim3(256), 0, st, a);
+    }
     return hipGetLastError();
 }
 
@@ -199,7 +238,10 @@ hipError_t launch_e(int epi, const GemvArgs& a, hipStream_t st) {
 hipError_t launch_gemm_pf(int fmt, int epi, const GemvArgs& a, hipStream_t st) {
     if (a.batch <= 0 || a.n_pad % 64 || a.C <= 0 || a.ksw > 1) return hipErrorInvalidValue;
     // byte offsets of the buffer loads are 32-bit
-    if ((int64_t)a.C * a.n_pad * 16 >= (1ll << 31) || (int64_t)a.batch * a.ldx * 4 >= (1ll << 31)) return hipErrorInvalidValue;
+    if ((int64_t)a.C * a.n_pad * 16 >= (1ll << 31) || (int64_t)a.batch * a.ldx * 4 >= (1ll << 31) ||
+        (int64_t)a.batch * a.C * 128 >= (1ll << 31))
+        return hipErrorInvalidValue;
+    if (a.xhl && a.ldx % 4) return hipErrorInvalidValue;  // the split pass loads 16 bytes at a time
     if (epi == EPI_QKV) {
         // a 128-row tile holds whole heads: hd 64, or hd 128 with 128-aligned sections
         if (!(a.hd == 64 || (a.hd == 128 && a.qd % 128 == 0 && a.kd % 128 == 0))) return hipErrorInvalidValue;
