@@ -203,6 +203,181 @@ __global__ void __launch_bounds__(256) k_gemm_pf(const GemvArgs a) {
     }
 }
 
+// LDS-staged variant for activations split once (a.xhl): per 32-wide K chunk the workgroup's 256
+// threads load the chunk's activation hi + lo of its MT tokens and its 128 weight rows, decode the
+// weights once to exact fp16 (q - 8) and store both, with the rows' fp16 group scales as f32, in
+// one of two LDS stages; every wave then reads its MFMA operands from LDS. Loads are requested
+// D chunks ahead into registers. Row strides are padded (80 B per weight row, 144 B per token) so
+// that the lanes of one 16-byte operand read fall in distinct banks. Arithmetic and accumulation
+// order are those of k_gemm_pf; the epilogue is the same.
+template <int FMT, int EPI>
+__global__ void __launch_bounds__(256, 2) k_gemm_pfl(const GemvArgs a) {
+    constexpr int NACC = EPI == EPI_SILU ? 2 : 1;
+    constexpr int TBW = NACC == 2 ? 2 : 4;  // 16-token blocks per wavefront
+    constexpr int MT = 2 * TBW * 16;        // tokens per workgroup
+    constexpr int ROWS = PF_ROWS;
+    constexpr int PH = 32;                  // tokens per epilogue phase
+    constexpr int AS = 80, BS = 144;        // LDS bytes per weight row (64 + pad), per token (128 + pad)
+    constexpr int A_BYTES = NACC * ROWS * AS, S_BYTES = NACC * ROWS * 4, B_BYTES = MT * BS;
+    constexpr int STAGE = A_BYTES + S_BYTES + B_BYTES;
+    constexpr int KB = MT * 8 / 256;        // 16-byte activation pieces per thread per chunk
+    constexpr int D = NACC == 2 ? 3 : 2;    // chunks in flight in registers (as many as fit 256 VGPRs)
+    static_assert((NACC * PH * ROWS + PH * ROWS) * 4 <= 2 * STAGE, "epilogue buffers fit the stages");
+    __shared__ __attribute__((aligned(16))) unsigned char lds[2 * STAGE];
+    __shared__ float rn[MT];
+    float* comb = (float*)lds;              // after the main loop: [NACC][PH][ROWS] sums
+    float* scratch = comb + NACC * PH * ROWS;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lr = lane & 15, lg = lane >> 4;
+    const int wn = wave & 1, wm = wave >> 1;
+    const int mtiles = (a.batch + MT - 1) / MT;
+    const int mt = blockIdx.x % mtiles, nt = blockIdx.x / mtiles;
+    const int tok0 = mt * MT;
+    const int C = a.C;
+
+    // loader roles: activation pieces q = tid + k * 256 (token q / 8, 16-byte part q % 8); weight
+    // row tid % 128 of matrix tid / 128 (threads below NACC * 128); clamped rows / tokens are never stored
+    const __amdgpu_buffer_rsrc_t rX =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.xhl, (short)0, (int)((int64_t)a.batch * C * 128), 0x00020000);
+    int vo_b[KB];
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+        const int q = threadIdx.x + k * 256;
+        vo_b[k] = min(tok0 + q / 8, a.batch - 1) * C * 128 + (q % 8) * 16;
+    }
+    const bool aload = (int)threadIdx.x < NACC * ROWS;
+    const int aj = NACC == 2 ? (int)threadIdx.x / ROWS : 0, arow = (int)threadIdx.x % ROWS;
+    const int grow = min(nt * ROWS + arow, a.n_pad - 1);
+    const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(aj == 0 ? a.W : a.W2), (short)0, C * a.n_pad * 16, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rS = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(aj == 0 ? a.S : a.S2), (short)0, C * a.n_pad * 2, 0x00020000);
+
+    struct Regs {
+        uint4 b[KB];
+        uint4 w;
+        uint32_t s;
+    };
+    Regs R[D];
+    auto request = [&](int c, Regs& r) {
+        const int cc = min(c, C - 1);
+#pragma unroll
+        for (int k = 0; k < KB; ++k)
+            r.b[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rX, vo_b[k], cc * 128, 0));
+        if (aload) {
+            r.w = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rW, grow * 16, cc * a.n_pad * 16, 0));
+            if constexpr (FMT == BH_Q4_G32) r.s = __builtin_amdgcn_raw_buffer_load_b16(rS, grow * 2, cc * a.n_pad * 2, 0);
+        }
+    };
+    auto store = [&](const Regs& r, int stage) {
+        unsigned char* st = lds + stage * STAGE;
+#pragma unroll
+        for (int k = 0; k < KB; ++k) {
+            const int q = threadIdx.x + k * 256;
+            *(uint4*)(st + A_BYTES + S_BYTES + (q / 8) * BS + (q % 8) * 16) = r.b[k];
+        }
+        if (aload) {
+            half8* dst = (half8*)(st + (aj * ROWS + arow) * AS);
+            dst[0] = dec8(r.w.x);
+            dst[1] = dec8(r.w.y);
+            dst[2] = dec8(r.w.z);
+            dst[3] = dec8(r.w.w);
+            if constexpr (FMT == BH_Q4_G32)
+                ((float*)(st + A_BYTES))[aj * ROWS + arow] = __half2float(__ushort_as_half((uint16_t)r.s));
+        }
+    };
+
+    f32x4 acc[NACC][4][TBW];
+#pragma unroll
+    for (int j = 0; j < NACC; ++j)
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int tb = 0; tb < TBW; ++tb) acc[j][rb][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](int stage) {
+        const unsigned char* st = lds + stage * STAGE;
+        half8 bh[TBW], bl[TBW];
+#pragma unroll
+        for (int tb = 0; tb < TBW; ++tb) {
+            const unsigned char* bp = st + A_BYTES + S_BYTES + (wm * TBW * 16 + tb * 16 + lr) * BS + lg * 16;
+            bh[tb] = *(const half8*)bp;
+            bl[tb] = *(const half8*)(bp + 64);
+        }
+#pragma unroll
+        for (int j = 0; j < NACC; ++j)
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                const half8 av = *(const half8*)(st + (j * ROWS + wn * 64 + rb * 16 + lr) * AS + lg * 16);
+                if constexpr (FMT == BH_Q4_G32) {
+                    const float4 sc = *(const float4*)(st + A_BYTES + (j * ROWS + wn * 64 + rb * 16 + 4 * lg) * 4);
+#pragma unroll
+                    for (int tb = 0; tb < TBW; ++tb) {
+                        f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bh[tb], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        t = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bl[tb], t, 0, 0, 0);
+                        acc[j][rb][tb][0] = fmaf(sc.x, t[0], acc[j][rb][tb][0]);
+                        acc[j][rb][tb][1] = fmaf(sc.y, t[1], acc[j][rb][tb][1]);
+                        acc[j][rb][tb][2] = fmaf(sc.z, t[2], acc[j][rb][tb][2]);
+                        acc[j][rb][tb][3] = fmaf(sc.w, t[3], acc[j][rb][tb][3]);
+                    }
+                } else {
+#pragma unroll
+                    for (int tb = 0; tb < TBW; ++tb) {
+                        acc[j][rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bh[tb], acc[j][rb][tb], 0, 0, 0);
+                        acc[j][rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bl[tb], acc[j][rb][tb], 0, 0, 0);
+                    }
+                }
+            }
+    };
+
+    // chunk c is in LDS stage c & 1 at the top of its iteration; chunks c + 1 .. c + D - 1 are in
+    // flight in register slots (c + 1) % D ..; slot c % D takes chunk c + D
+#pragma unroll
+    for (int u = 0; u < D; ++u) request(u, R[u]);
+    {
+        const GemvArgs at = gemv_tokens(a, tok0, min(MT, a.batch - tok0));
+        if (threadIdx.x < MT) rn[threadIdx.x] = (at.ssq_in && (int)threadIdx.x < at.batch) ? stream_rnorm(at, threadIdx.x) : 1.0f;
+    }
+    store(R[0], 0);
+    __syncthreads();
+    for (int c0 = 0; c0 < C; c0 += D) {
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+            const int c = c0 + u;
+            if (c >= C) break;  // uniform
+            request(c + D, R[u]);
+            compute(c & 1);
+            if (c + 1 < C) store(R[(u + 1) % D], (c + 1) & 1);
+            __syncthreads();
+        }
+    }
+
+    // Epilogue in phases of 32 tokens, as k_gemm_pf (comb / scratch now over the stages).
+    constexpr float FIN = FMT == BH_Q4_ROW ? 16.0f : 1.0f;
+    for (int ph = 0; ph < MT / PH; ++ph) {
+        __syncthreads();
+#pragma unroll
+        for (int tb = 0; tb < TBW; ++tb) {
+            const int t = wm * TBW * 16 + tb * 16;
+            if (t / PH != ph) continue;
+#pragma unroll
+            for (int j = 0; j < NACC; ++j)
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        comb[(j * PH + (t % PH) + lr) * ROWS + wn * 64 + rb * 16 + 4 * lg + v] = acc[j][rb][tb][v] * FIN;
+        }
+        __syncthreads();
+        const int b0 = tok0 + ph * PH;
+        if (b0 >= a.batch) break;  // uniform
+        const GemvArgs ap = gemv_tokens(a, b0, min(PH, a.batch - b0));
+        run_epilogue<FMT, PH, EPI, ROWS>(ap, comb, scratch, rn + ph * PH, (int64_t)nt * ROWS);
+    }
+}
+
 template <int FMT, int EPI>
 hipError_t launch_t(const GemvArgs& a, hipStream_t st) {
     constexpr int NACC = EPI == EPI_SILU ? 2 : 1;
@@ -215,7 +390,7 @@ hipError_t launch_t(const GemvArgs& a, hipStream_t st) {
         const int64_t groups = (int64_t)a.batch * a.C * 4;
         launch_kernel(k_split_act, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, st, a.x, a.ldx, a.batch, a.C,
                       a.xhl);
-        launch_kernel((k_gemm_pf<FMT, EPI, true>), dim3(mtiles * ntiles), dim3(256), 0, st, a);
+        launch_kernel((k_gemm_pfl<FMT, EPI>), dim3(mtiles * ntiles), dim3(256), 0, st, a);
     } else {
         launch_kernel((k_gemm_pf<FMT, EPI, false>), dim3(mtiles * ntiles), dim3(256), 0, st, a);
     }
