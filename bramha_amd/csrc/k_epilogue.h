@@ -102,10 +102,15 @@ template <int TOT>
 __device__ __forceinline__ bool split_reduce(const GemvArgs& a, float* comb, int tile, int kws) {
     __shared__ int s_last;
     const int ksw = a.ksw;
+    static_assert(TOT % 2 == 0, "partials move as 64-bit pairs");
+    __syncthreads();  // a thread publishes a pair of sums written by two threads
     float* mine = a.part + (int64_t)(tile * ksw + kws) * TOT;
-    float sink = 0.f;
-    for (int i = threadIdx.x; i < TOT; i += blockDim.x)
-        sink += __hip_atomic_exchange(&mine[i], comb[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned long long sink = 0;
+    for (int i = 2 * threadIdx.x; i < TOT; i += 2 * blockDim.x) {
+        const unsigned long long v =
+            (unsigned long long)__float_as_uint(comb[i]) | ((unsigned long long)__float_as_uint(comb[i + 1]) << 32);
+        sink += __hip_atomic_exchange((unsigned long long*)&mine[i], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     asm volatile("" ::"v"(sink));  // the returned values are consumed: the exchanges have completed
     __syncthreads();
     if (threadIdx.x == 0)
@@ -113,16 +118,21 @@ __device__ __forceinline__ bool split_reduce(const GemvArgs& a, float* comb, int
     __syncthreads();
     if (!s_last) return false;
     const float* all = a.part + (int64_t)tile * ksw * TOT;
-    for (int i = threadIdx.x; i < TOT; i += blockDim.x) {
+    for (int i = 2 * threadIdx.x; i < TOT; i += 2 * blockDim.x) {
         // all splits' loads in flight at once (index clamped in bounds), added in split order
-        float v[MAX_KSW];
+        unsigned long long v[MAX_KSW];
 #pragma unroll
         for (int k = 0; k < MAX_KSW; ++k)
-            v[k] = __hip_atomic_load(&all[(int64_t)min(k, ksw - 1) * TOT + i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        float sum = 0.f;
+            v[k] = __hip_atomic_load((const unsigned long long*)&all[(int64_t)min(k, ksw - 1) * TOT + i], __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+        float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-        for (int k = 0; k < MAX_KSW; ++k) sum += k < ksw ? v[k] : 0.f;
-        comb[i] = sum;
+        for (int k = 0; k < MAX_KSW; ++k) {
+            s0 += k < ksw ? __uint_as_float((unsigned)v[k]) : 0.f;
+            s1 += k < ksw ? __uint_as_float((unsigned)(v[k] >> 32)) : 0.f;
+        }
+        comb[i] = s0;
+        comb[i + 1] = s1;
     }
     if (threadIdx.x == 0) __hip_atomic_store(&a.tile_cnt[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return true;
