@@ -37,7 +37,7 @@ typedef enum {
     BH_ERR_OOM = -4,          /* device allocation failed */
     BH_ERR_NOT_FOUND = -5,    /* unknown tensor name / registry key */
     BH_ERR_INJECTED = -6,     /* failure forced by bh_debug_inject_fault */
-    BH_ERR_UNSUPPORTED = -7,  /* shape or format this build does not run */
+    BH_ERR_UNSUPPORTED = -7,  /* shape or format the backend does not run */
     BH_ERR_CAPACITY = -8      /* KV rows, slots or batch size exceeded */
 } bh_status;
 

@@ -1,6 +1,6 @@
 """The oracle: a CPU restatement of the reference's quantized decode path.
 
-TEST INFRASTRUCTURE ONLY. It is the checker the HIP backend is compared against;
+TEST INFRASTRUCTURE ONLY. It is what the HIP backend is compared against;
 only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import it.
 The restatement is oracle/oracle.cpp (built by oracle/Makefile into liboracle.so);
 every function there cites the reference file:line it follows.

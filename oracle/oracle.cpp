@@ -1,8 +1,8 @@
 // oracle.cpp — CPU restatement of the reference's quantized decode path.
 //
-// TEST INFRASTRUCTURE ONLY. This library is the checker for the HIP backend in
-// bramha_amd/: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
-// leg may load it. Nothing in the product links or calls it.
+// TEST INFRASTRUCTURE ONLY. The HIP backend in bramha_amd/ is compared against this
+// library; only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+// load it. Nothing in the product links or calls it.
 //
 // The reference (akshaybhlrp/bramha) is Rust and cannot be built in this image,
 // so every function below restates one reference function, following its

@@ -1,6 +1,6 @@
 """GPU decoder parity against the oracle's decode loop.
 
-Bars (north star): greedy ids equal; per-step raw logits within 2e-2 max-abs and 1e-3
+Bars: greedy ids equal; per-step raw logits within 2e-2 max-abs and 1e-3
 relative L2. The tiny configurations with f32 KV are held to a much tighter 1e-4
 relative bound so that indexing mistakes cannot hide inside the tolerance.
 With an fp16 KV cache the device sees rounded K/V rows that the f32 oracle does not;
