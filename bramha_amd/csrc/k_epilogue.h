@@ -92,6 +92,40 @@ struct RnormReq {
     }
 };
 
+// The same norm factors for the VALU GEMV (B <= 8, one wave of 64 lanes covers B * NV tiles):
+// lane b * NV + k of wave 0 requests tile k of token b, one register per lane, and in finish()
+// lane b gathers its NV tiles in order through cross-lane reads. (Per-thread arrays would hold
+// NV registers through the main loop, and at B = 1 the compiler turns them into scalar loads
+// issued one after another.) All lanes of wave 0 call both; finish() is followed by a
+// __syncthreads() before rn is read.
+template <int B, int NV>
+struct RnormLanes {
+    static_assert(B * NV <= 64, "one wave");
+    float v = 0.f;
+    __device__ __forceinline__ void request(const GemvArgs& a) {
+        const int b = (int)threadIdx.x / NV, k = (int)threadIdx.x % NV;
+        if (a.ssq_in && (int)threadIdx.x < B * NV && b < a.batch)
+            v = a.ssq_in[(int64_t)b * a.ssq_tiles + min(k, a.ssq_tiles - 1)];
+    }
+    __device__ __forceinline__ void finish(const GemvArgs& a, float* rn) const {
+        if (threadIdx.x >= 64) return;  // wave 0
+        const int b = (int)threadIdx.x;
+        float t = 0.f;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const float x = __shfl(v, (b % B) * NV + k);
+            if (k < a.ssq_tiles) t += x;
+        }
+        if (b >= B) return;
+        if (!a.ssq_in || b >= a.batch) {
+            rn[b] = 1.0f;
+            return;
+        }
+        t = rnorm_sum(a.ssq_in + (int64_t)b * a.ssq_tiles, a.ssq_tiles, NV, t);
+        rn[b] = 1.0f / sqrtf(t / a.norm_n + a.eps);
+    }
+};
+
 // K split over workgroups (a.ksw > 1): publish this split's TOT sums and let the tile's last
 // workgroup add all splits in split order; returns false in every other workgroup, which then
 // exits. The sums are published with agent-scope atomic exchanges and read back with agent-scope
@@ -219,9 +253,20 @@ struct EpiPre {
     float2 cs = {1.f, 0.f};                             // RoPE (cos, sin)
     int64_t kvrow = 0;                                  // KV row of the token
     int cnt = 0;                                        // penalty count
-    __device__ __forceinline__ void load(const GemvArgs& a, int64_t row0) {
+    // All threads call it; thread r < rows takes weight row row0 + r. The token's position, KV
+    // offset and slot are read first, outside the per-row branch, so they are scalar loads: a
+    // vector load there would make its dependent loads wait for every earlier load (the first
+    // weight stage included).
+    __device__ __forceinline__ void load(const GemvArgs& a, int64_t row0, int rows) {
+        int p = 0, slot0 = 0;
+        int64_t boff0 = 0;
+        if constexpr (EPI == EPI_QKV) {
+            p = a.pos[0];
+            boff0 = a.boff[0];
+        }
+        if constexpr (EPI == EPI_LMHEAD) slot0 = a.slot[0];
         const int64_t nn = row0 + threadIdx.x;
-        if (nn >= a.N) return;
+        if ((int)threadIdx.x >= rows || nn >= a.N) return;
         if constexpr (EPI == EPI_STORE) {
             if (a.bias) bias = a.bias[nn];
         } else if constexpr (EPI == EPI_RESNORM) {
@@ -233,15 +278,14 @@ struct EpiPre {
             const int sec = nn < a.qd ? 0 : (nn < a.qd + a.kd ? 1 : 2);
             const int loc = (int)nn - (sec == 0 ? 0 : (sec == 1 ? a.qd : a.qd + a.kd));
             const int d = loc % a.hd;
-            const int p = a.pos[0];
             if (a.bias) {
                 bias = a.bias[nn];
                 if (sec < 2) pbias = a.bias[nn + (d < half ? half : -half)];
             }
             if (sec < 2) cs = a.rope[(int64_t)p * half + (d < half ? d : d - half)];
-            if (sec > 0) kvrow = a.boff[0] + kv_phys_row(a.kv, p);
+            if (sec > 0) kvrow = boff0 + kv_phys_row(a.kv, p);
         } else if constexpr (EPI == EPI_LMHEAD) {
-            cnt = a.pen[(int64_t)a.slot[0] * a.vocab + nn];
+            cnt = a.pen[(int64_t)slot0 * a.vocab + nn];
         }
     }
 };

@@ -57,22 +57,21 @@ __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
 
     {
         float acc[NACC][B];
-        float touch = 0.f;
-        RnormReq<B, B == 1 ? RN_U : 8> rq;  // fewer early tiles where registers are tight
+        float touch[TOUCH_ROWS];
+        RnormLanes<B, (B <= 4 ? RN_U : 8)> rq;
         stream_chunks<FMT, B, NACC, U, CP>(a, nl, c0, c1, acc, [&] {
             // the activation touch (bs1 decode step: 1232 -> 1291 tok/s), the norm factors and the
             // batch-1 epilogue operands load while the first weight stage is in flight
-            touch = touch_activations<B, E>(a, wc0, wc1);
+            touch_activations<B, E>(a, wc0, wc1, touch);
             rq.request(a);
-            if constexpr (B == 1)
-                if (threadIdx.x < ROWS) pre.load(a, (int64_t)tile * ROWS);
+            if constexpr (B == 1) pre.load(a, (int64_t)tile * ROWS, ROWS);
         });
 #pragma unroll
         for (int j = 0; j < NACC; ++j)
 #pragma unroll
             for (int b = 0; b < B; ++b) comb[kw * TOT + (j * B + b) * ROWS + r] = acc[j][b];
         rq.finish(a, rn);
-        asm volatile("" ::"v"(touch));
+        touch_sink<B>(touch);
     }
 
     // ---- combine the K-split partial sums in a fixed order ----

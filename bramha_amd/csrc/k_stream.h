@@ -150,17 +150,25 @@ __device__ __forceinline__ void stream_chunks(const GemvArgs& a, int64_t nl, int
     }
 }
 
-// Touch of the activations of chunks [wc0, wc1) of B rows, one vector load per 128-byte
-// line, so that the scalar loads of the main loop hit L2: the activations were just written by
-// the previous kernel, often on another XCD. The returned value must be consumed (an empty asm
-// operand) after the main loop so nothing waits on the loads early.
+// Touch of the activations of chunks [wc0, wc1) of B rows: one vector load per 128-byte line
+// (clamped, unconditional: one line per thread and row covers 32 blockDim floats, the lines past
+// it are left to the scalar loads), so that the scalar loads of the main loop hit L2: the
+// activations were just written by the previous kernel, often on another XCD. Each value stays
+// in its own register and must only be consumed after the main loop (`touch_sink`); any earlier
+// use would wait on the load, and with it on the weight stage issued before it.
+// At most TOUCH_ROWS rows are touched: the registers are held through the main loop.
+constexpr int TOUCH_ROWS = 2;
 template <int B, int E>
-__device__ __forceinline__ float touch_activations(const GemvArgs& a, int wc0, int wc1) {
-    float touch = 0.f;
+__device__ __forceinline__ void touch_activations(const GemvArgs& a, int wc0, int wc1, float (&t)[TOUCH_ROWS]) {
     const int nx = (wc1 - wc0) * E;
-    for (int bb = 0; bb < B; ++bb)
-        for (int i2 = threadIdx.x * 32; i2 < nx; i2 += blockDim.x * 32) touch += a.x[(int64_t)bb * a.ldx + wc0 * E + i2];
-    return touch;
+    const int i2 = min((int)threadIdx.x * 32, max(nx - 1, 0));
+#pragma unroll
+    for (int bb = 0; bb < TOUCH_ROWS; ++bb) t[bb] = a.x[(int64_t)min(bb, B - 1) * a.ldx + wc0 * E + i2];
+}
+template <int B>
+__device__ __forceinline__ void touch_sink(const float (&t)[TOUCH_ROWS]) {
+#pragma unroll
+    for (int bb = 0; bb < (B < TOUCH_ROWS ? B : TOUCH_ROWS); ++bb) asm volatile("" ::"v"(t[bb]));
 }
 
 }  // namespace bh
