@@ -556,7 +556,7 @@ static int attn_args(bh_ctx* ctx, const float* q, const void* k, const void* v, 
     a.nq = n_q;
     a.nkv = n_kv;
     a.hd = head_dim;
-    attn_plan(std::max(max_len, 1), batch, n_kv, &a.splits, &a.split_rows);
+    attn_plan(std::max(max_len, 1), batch, n_kv, head_dim, &a.splits, &a.split_rows);
     if (a.splits > 1) {
         const size_t need = (size_t)batch * n_q * a.splits * (head_dim + 2) * 4;
         if (need > ctx->attn_part_bytes) {

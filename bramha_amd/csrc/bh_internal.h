@@ -272,7 +272,7 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
 // Head layouts the attention kernel is built for: hd 64/128, n_q/n_kv in {1, 2, 4, 7, 8}.
 bool attn_supported(int nq, int nkv, int hd);
 // Split plan for contexts up to max_len rows.
-void attn_plan(int max_len, int batch, int nkv, int* splits, int* split_rows);
+void attn_plan(int max_len, int batch, int nkv, int hd, int* splits, int* split_rows);
 
 // ---------------------------------------------------------------------------
 // Host helpers (bh_host.cpp)

@@ -751,7 +751,7 @@ int bh_model_prefill(bh_model* m, int slot, const uint32_t* tokens, int n) {
         if (e == hipSuccess) e = hipMemcpyAsync(m->d_ppos, pos, (size_t)M * 4, hipMemcpyHostToDevice, m->st);
         if (e == hipSuccess) e = hipMemcpyAsync(m->d_pslot, sl, (size_t)M * 4, hipMemcpyHostToDevice, m->st);
         int splits, rows;
-        attn_plan(pos[M - 1] + 1, M, m->c.n_kv_heads, &splits, &rows);
+        attn_plan(pos[M - 1] + 1, M, m->c.n_kv_heads, m->c.head_dim, &splits, &rows);
         if (e == hipSuccess)
             e = launch_embed(m->embed, m->d_ptok, m->L[0].ln1, m->x, m->xw, m->ssq, m->ssq_tiles, nullptr, M, m->st);
         if (e == hipSuccess) e = forward(m, M, false, splits, rows);
@@ -817,7 +817,7 @@ static int decode_locked(bh_model* m, int n_steps, uint32_t* ids_out, float* raw
     int rc = check_decode_room(m, n_steps);
     if (rc) return rc;
     int splits, rows;
-    attn_plan(decode_len_bound(m, n_steps), m->B, m->c.n_kv_heads, &splits, &rows);
+    attn_plan(decode_len_bound(m, n_steps), m->B, m->c.n_kv_heads, m->c.head_dim, &splits, &rows);
     hipError_t e = hipSuccess;
     if (!m->gexec || m->g_B != m->B || m->g_splits != splits || m->g_rows != rows) {
         drop_graph(m);
@@ -918,7 +918,7 @@ int bh_model_time_kernels(bh_model* m, int n_steps, double* mean_us, int64_t* la
     int rc = check_decode_room(m, n_steps);
     if (rc) return rc;
     int splits, rows;
-    attn_plan(decode_len_bound(m, n_steps), m->B, m->c.n_kv_heads, &splits, &rows);
+    attn_plan(decode_len_bound(m, n_steps), m->B, m->c.n_kv_heads, m->c.head_dim, &splits, &rows);
     std::vector<double> tot(BH_K_COUNT, 0.0);
     std::vector<int64_t> cnt(BH_K_COUNT, 0);
     hipError_t e = decode_start(m);

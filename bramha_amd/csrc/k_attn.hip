@@ -811,14 +811,14 @@ hipError_t launch_g(const AttnArgs& a, hipStream_t st) {
 
 // Context split. Up to 1024 rows a (row, KV head) stays in one workgroup (each wave takes at
 // most two 64-row tiles, cheaper than a merge). Longer contexts are cut into splits of at
-// least 512 rows, as many as it takes to give the chip about one workgroup per CU, at most 128:
-// the merge's last workgroup reads every split's partials, so fewer, longer splits win (T =
-// 32768: 21.9 -> 14.5 us at batch 1, 37.8 -> 31.6 at 8; T = 4096, batch 32: 24.8 -> 19.7 us
-// against 512 workgroups of 256-row splits). Splits of more than 4 tiles run 8 waves per
-// workgroup, shorter ones 4.
+// least 64 KiB of K and V per head (512 rows at head_dim 64, 256 at 128), as many as it takes
+// to give the chip about one workgroup per CU, at most 128: the merge's last workgroup reads
+// every split's partials, so fewer, longer splits win (T = 32768: 21.9 -> 14.5 us at batch 1,
+// 37.8 -> 31.6 at 8; T = 4096, batch 32: 24.8 -> 19.7 us against 512 workgroups of 256-row
+// splits). Splits of more than 4 tiles run 8 waves per workgroup, shorter ones 4.
 constexpr int ATTN_TARGET_WG = 256;
-constexpr int ATTN_MIN_ROWS = 512;
-void attn_plan(int max_len, int batch, int nkv, int* splits, int* split_rows) {
+constexpr int ATTN_MIN_ROWS_HD64 = 512;
+void attn_plan(int max_len, int batch, int nkv, int hd, int* splits, int* split_rows) {
     // the bound is rounded up (256, 512, 1024, then multiples of 1024) so that a decode graph
     // captured for it stays valid while the context grows: rows past a sequence's length cost a
     // skipped tile or an empty split, a new plan costs a graph capture
@@ -832,7 +832,7 @@ void attn_plan(int max_len, int batch, int nkv, int* splits, int* split_rows) {
     const int heads = std::max(batch * nkv, 1);
     const int want = std::max(1, (ATTN_TARGET_WG + heads - 1) / heads);
     int rows = (max_len + want - 1) / want;
-    rows = std::max(rows, ATTN_MIN_ROWS);
+    rows = std::max(rows, ATTN_MIN_ROWS_HD64 * 64 / std::max(hd, 64));
     rows = std::max(rows, (max_len + MAX_SPLITS - 1) / MAX_SPLITS);
     rows = (rows + 63) / 64 * 64;
     *splits = (max_len + rows - 1) / rows;
