@@ -36,7 +36,8 @@ BH_F32, BH_Q8_ROW, BH_Q4_ROW, BH_Q4_G32 = 0, 1, 2, 3
 BH_OP_ANY, BH_OP_MATVEC, BH_OP_UPLOAD, BH_OP_GEMV, BH_OP_DECODE = 0, 1, 2, 3, 4
 
 # kernel classes for per-kernel timing
-KCLASSES = ["gemv_qkv", "attention", "gemv_o", "gemv_gate_up", "gemv_down", "lm_head", "rmsnorm", "other"]
+KCLASSES = ["gemv_qkv", "attention", "gemv_o", "gemv_gate_up", "gemv_down", "lm_head", "rmsnorm", "other",
+            "attn_o"]
 BH_K_COUNT = len(KCLASSES)
 
 

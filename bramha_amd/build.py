@@ -18,6 +18,7 @@ SOURCES = [
     "csrc/k_gemm.hip",
     "csrc/k_prefill.hip",
     "csrc/k_attn.hip",
+    "csrc/k_attn_o.hip",
     "csrc/k_ops.hip",
     "csrc/bh_host.cpp",
     "csrc/bh_api.cpp",

@@ -273,6 +273,10 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
 bool attn_supported(int nq, int nkv, int hd);
 // Split plan for contexts up to max_len rows.
 void attn_plan(int max_len, int batch, int nkv, int hd, int* splits, int* split_rows);
+// Batch-1 decode: attention, O projection and residual epilogue in one launch (k_attn_o.hip),
+// for the configurations attn_o_fusable accepts (Q4_G32, fp16 cache, short contexts).
+bool attn_o_fusable(int fmt, const AttnArgs& at, const GemvArgs& o);
+hipError_t launch_attn_o(int fmt, const AttnArgs& at, const GemvArgs& o, hipStream_t st);
 
 // ---------------------------------------------------------------------------
 // Host helpers (bh_host.cpp)

@@ -238,8 +238,6 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
                 at.cap_rows = std::min<int64_t>(at.cap_rows, m->cap_h[m->bslots[b]]);
             }
         }
-        e = timed(m, BH_K_ATTN, [&] { return launch_attention(at, st); });
-        if (e != hipSuccess) break;
         GemvArgs o;
         weight_args(m, o, w.o);
         o.x = m->att;
@@ -247,8 +245,16 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
         o.bias = c.o_bias ? w.bo : nullptr;
         o.batch = M;
         stream_output(m, o, w.ln2);
-        e = timed(m, BH_K_GEMV_O, [&] { return launch_gemv(c.wfmt, EPI_RESNORM, o, st); });
-        if (e != hipSuccess) break;
+        if (decode && M == 1 && attn_o_fusable(c.wfmt, at, o)) {
+            // batch 1, short context: attention, O projection and residual add in one launch
+            e = timed(m, BH_K_ATTN_O, [&] { return launch_attn_o(c.wfmt, at, o, st); });
+            if (e != hipSuccess) break;
+        } else {
+            e = timed(m, BH_K_ATTN, [&] { return launch_attention(at, st); });
+            if (e != hipSuccess) break;
+            e = timed(m, BH_K_GEMV_O, [&] { return launch_gemv(c.wfmt, EPI_RESNORM, o, st); });
+            if (e != hipSuccess) break;
+        }
         GemvArgs gu;
         weight_args(m, gu, w.gate);
         gu.W2 = w.up.q;
@@ -965,14 +971,19 @@ int bh_model_kernel_bytes(bh_model* m, int kclass, double* bytes) {
         case BH_K_LM_HEAD:  // tied table, xw in; logits out, penalty counts read
             *bytes = weight_bytes(m->have_lm_head ? m->lm_head : m->embed) + B * (H + T) * 4 + B * (double)c.vocab * 4 + B * (double)c.vocab * 2;
             return BH_OK;
-        case BH_K_ATTN: {
+        case BH_K_ATTN:
+        case BH_K_ATTN_O: {
             double rows = 0;
             for (int b = 0; b < m->B; ++b) {
                 int64_t len = m->len_h[m->bslots[b]];
                 if (c.max_context > 0) len = std::min<int64_t>(len, c.max_context);
                 rows += (double)len;
             }
-            *bytes = rows * 2 * KD * kvb + 2 * B * QD * 4;
+            if (kclass == BH_K_ATTN) {  // K/V rows and q in, attention out
+                *bytes = rows * 2 * KD * kvb + 2 * B * QD * 4;
+            } else {  // K/V rows and q in; O weights, x read and written, xw and ssq out, norm weight
+                *bytes = rows * 2 * KD * kvb + B * QD * 4 + weight_bytes(w.o) + B * (3 * H + T) * 4 + H * 4;
+            }
             return BH_OK;
         }
         default: *bytes = 0; return BH_OK;

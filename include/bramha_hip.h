@@ -250,9 +250,10 @@ void* bh_model_stream(bh_model* m);
  * class `kclass` (BH_K_*) is launched with hipExtLaunchKernelGGL, which records a pair of HIP
  * events at the kernel's own start and end on the model's stream. Returns the mean duration in
  * microseconds and the launch count per class. (BH_K_NORM has no launches: the RMSNorm is folded
- * into the projections.) */
+ * into the projections. BH_K_ATTN_O is the batch-1 decode launch that computes the attention, the
+ * O projection and the residual add together; where it runs, BH_K_ATTN and BH_K_GEMV_O do not.) */
 enum { BH_K_GEMV_QKV = 0, BH_K_ATTN = 1, BH_K_GEMV_O = 2, BH_K_GEMV_GATEUP = 3, BH_K_GEMV_DOWN = 4,
-       BH_K_LM_HEAD = 5, BH_K_NORM = 6, BH_K_OTHER = 7, BH_K_COUNT = 8 };
+       BH_K_LM_HEAD = 5, BH_K_NORM = 6, BH_K_OTHER = 7, BH_K_ATTN_O = 8, BH_K_COUNT = 9 };
 int bh_model_time_kernels(bh_model* m, int n_steps, double* mean_us /*[BH_K_COUNT]*/,
                           int64_t* launches /*[BH_K_COUNT]*/);
 /* Algorithmic HBM bytes one launch of kernel class `kclass` reads and writes at the

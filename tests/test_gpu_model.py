@@ -198,6 +198,32 @@ def test_graph_replay_matches_single_steps(plane):
     assert np.array_equal(a, b) and np.array_equal(la, lb)
 
 
+@pytest.mark.parametrize("shape,plen", [("gqa7", 20), ("gqa7", 100), ("gqa7", 300), ("hd128", 40), ("hd128", 200)])
+def test_batch1_attention_o_launch_matches_batched_path(plane, shape, plen):
+    """Batch-1 decode over an fp16 cache computes attention, the O projection and the residual
+    add in one launch; a batch of two runs them as separate kernels. The same prompt decoded
+    both ways gives the same ids and logits to 1e-4 (the launches differ only in summation
+    order). Context bounds of 64, 128 and 512 rows (one tile per attention wave at 1, 2 and 8
+    waves per KV head); head_dim 128 with two KV heads at bounds of 64 (2 waves of one tile)
+    and 256 rows (4 waves of two tiles)."""
+    if shape == "hd128":
+        cfg = tiny_cfg(Q4_G32, Q4_G32, kv_f16=True, hidden=512, n_heads=4, n_kv_heads=2, head_dim=128, ffn=768)
+    else:
+        cfg = tiny_cfg(Q4_G32, Q4_G32, gqa7=True, kv_f16=True)
+    _, gm = _pair(plane, cfg, seed=41)
+    p = prompt(plen, cfg.vocab, seed=42)
+    q = prompt(plen // 2 + 3, cfg.vocab, seed=43)
+    for slot, pp in ((0, p), (1, p), (2, q)):
+        gm.seq_open(slot, (plen + 64) // 64 * 64 + 64)
+        gm.prefill(slot, pp[:-1])
+    gm.decode_setup([0], [p[-1]])
+    a, la = gm.decode(8, want_logits=True)
+    gm.decode_setup([1, 2], [p[-1], q[-1]])
+    b, lb = gm.decode(8, want_logits=True)
+    assert np.array_equal(a[:, 0], b[:, 0])
+    assert np.max(np.abs(la[:, 0] - lb[:, 0])) <= 1e-4 * max(1.0, np.abs(lb[:, 0]).max())
+
+
 def _full_model(cfg, seed):
     return list(synth_weights(cfg, seed=seed))
 
