@@ -18,6 +18,12 @@
 // their latency hides under the attention. Partial sums are combined in wave order and the
 // residual epilogue of k_epilogue.h finishes the tile. Deterministic: no atomics.
 //
+// Where waves are left over from the attention (PRE), those waves alone take the projection:
+// they request and decode their weights to exact fp16 (q - 8) while the attention runs, and
+// after the merge spend one mixed-precision FMA per weight instead of the decode's 2.6 VALU
+// operations. fma(x, q - 8, p) scaled by s is fma(x, 16 (q - 8), p) scaled by s / 16 bit for bit
+// (power-of-two scaling commutes with rounding), so both variants compute k_gemv's values.
+//
 // Used when the projection needs no K split over workgroups (fewer than 64 chunks of K), for
 // Q4_G32 weights, an fp16 cache and contexts of at most 256 KiB of K and V.
 #include "bh_internal.h"
@@ -34,8 +40,30 @@ namespace {
 constexpr int AO_WAVES = 8;                  // waves per workgroup (256 VGPRs each)
 constexpr int64_t AO_KV_BYTES = 256 * 1024;  // K + V bytes of the context, per workgroup
 
-// One workgroup of AO_WAVES waves per 64-row tile of the projection. U: chunks per wave.
-template <int HD, int G, int U>
+// The slot of dec8's output (k_mfma.h) that holds element e of a dword's 8 nibbles.
+__host__ __device__ constexpr int kslot(int e) { return e < 4 ? 2 * (e ^ 1) : 2 * ((e - 4) ^ 1) + 1; }
+constexpr bool kslot_inverts_kperm() {
+    for (int e = 0; e < 8; ++e)
+        if (kperm(kslot(e)) != e) return false;
+    return true;
+}
+static_assert(kslot_inverts_kperm(), "kslot must invert kperm");
+
+// The 32 activations of one chunk from LDS (128-byte aligned) as 16-byte reads.
+__device__ __forceinline__ void load_chunk_x(const float* x, float (&xb)[32]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float4 t = ((const float4*)x)[i];
+        xb[4 * i] = t.x;
+        xb[4 * i + 1] = t.y;
+        xb[4 * i + 2] = t.z;
+        xb[4 * i + 3] = t.w;
+    }
+}
+
+// One workgroup of AO_WAVES waves per 64-row tile of the projection. U: chunks per projection
+// wave. PRE: the waves past the attention waves take the projection, with pre-decoded weights.
+template <int HD, int G, int U, bool PRE>
 __global__ void __launch_bounds__(64 * AO_WAVES) k_attn_o(const AttnArgs at, const GemvArgs a, const int nwh) {
     using AW = AttnWave<HD, 1, false>;
     constexpr int KC = HD / 32;  // 32-wide head-dim chunks of the score product
@@ -56,8 +84,11 @@ __global__ void __launch_bounds__(64 * AO_WAVES) k_attn_o(const AttnArgs at, con
     const int tile = blockIdx.x;
     const int64_t n = (int64_t)tile * 64 + lane;
     const int64_t nl = n < a.n_pad ? n : (int64_t)a.n_pad - 1;
-    const int per = (a.C + NW - 1) / NW;
-    const int c0 = wave * per, c1 = min(a.C, c0 + per);
+    // projection waves: every wave, or (PRE) waves na .. NW - 1
+    const int pw = PRE ? wave - na : wave;
+    const int npw = PRE ? NW - na : NW;
+    const int per = (a.C + npw - 1) / npw;
+    const int c0 = pw * per, c1 = min(a.C, c0 + per);
 
     // the wave's projection weights and scales, one stage of U chunks (clamped, unconditional)
     const __amdgpu_buffer_rsrc_t rW =
@@ -101,7 +132,7 @@ __global__ void __launch_bounds__(64 * AO_WAVES) k_attn_o(const AttnArgs at, con
         const int tfirst = aw.wv * AW::TR;
         const bool spec = aw.tiled && tfirst + AW::TR <= at.cap_rows;
         if (spec) aw.load_full(aw.A, tfirst);
-        fetch_w();
+        if constexpr (!PRE) fetch_w();
         pre.load(a, (int64_t)tile * 64, 64);
         int len = at.pos[0] + 1;
         if (at.kv.max_context > 0) len = min(len, at.kv.max_context);
@@ -140,6 +171,20 @@ __global__ void __launch_bounds__(64 * AO_WAVES) k_attn_o(const AttnArgs at, con
         fetch_w();
         pre.load(a, (int64_t)tile * 64, 64);
     }
+    // PRE: the projection waves' weights as exact fp16 q - 8 (dec8 slot order), decoded while
+    // the attention waves run
+    half8 wd[PRE ? U : 1][4];
+    if constexpr (PRE) {
+        if (pw >= 0) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                wd[u][0] = dec8(wq[u].x);
+                wd[u][1] = dec8(wq[u].y);
+                wd[u][2] = dec8(wq[u].z);
+                wd[u][3] = dec8(wq[u].w);
+            }
+        }
+    }
     __syncthreads();
 
     // merge the waves of each KV head (log-sum-exp weights, in wave order) into the output
@@ -165,12 +210,28 @@ __global__ void __launch_bounds__(64 * AO_WAVES) k_attn_o(const AttnArgs at, con
     // the projection over the wave's chunks, activations broadcast from LDS (the arithmetic and
     // order of k_stream.h's chunk loop)
     float acc = 0.f;
+    if constexpr (PRE) {
+        if (pw >= 0) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
+            for (int u = 0; u < U; ++u) {
+                if (c0 + u < c1) {
+                    float xb[E];
+                    load_chunk_x(xs + (c0 + u) * E, xb);
+                    float p = 0.f;
+#pragma unroll
+                    for (int e = 0; e < E; ++e) p = fmaf(xb[e], (float)wd[u][e / 8][kslot(e % 8)], p);
+                    acc = fmaf(p, __half2float(__ushort_as_half((uint16_t)ws[u])), acc);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < (PRE ? 0 : U); ++u) {
         if (c0 + u < c1) {
             float v[E];
             decode<BH_Q4_G32>(wq[u], v);
-            const float* xb = xs + (c0 + u) * E;
+            float xb[E];
+            load_chunk_x(xs + (c0 + u) * E, xb);
             float p = 0.f;
 #pragma unroll
             for (int e = 0; e < E; ++e) p = fmaf(xb[e], v[e], p);
@@ -190,6 +251,7 @@ __global__ void __launch_bounds__(64 * AO_WAVES) k_attn_o(const AttnArgs at, con
 
 struct AoPlan {
     int nwh = 0, u = 0;
+    bool pre = false;
     size_t shm = 0;
 };
 
@@ -210,9 +272,12 @@ bool ao_plan(int fmt, const AttnArgs& at, const GemvArgs& o, AoPlan* p) {
     // instead of 8.8 us with 2 waves instead of 4)
     const int tr = 32 * KvTile<64>::NJ * 64 / at.hd;  // rows per tile
     p->nwh = std::max(1, std::min((int)((rows + tr - 1) / tr), AO_WAVES / at.nkv));
-    const int per = (o.C + AO_WAVES - 1) / AO_WAVES;
-    p->u = per <= 4 ? 4 : 8;
     const int na = at.nkv * p->nwh;
+    // the waves left over from the attention take the projection when they hold at most 8 chunks
+    // each as fp16
+    p->pre = na < AO_WAVES && (o.C + AO_WAVES - na - 1) / (AO_WAVES - na) <= 8;
+    const int per = p->pre ? (o.C + AO_WAVES - na - 1) / (AO_WAVES - na) : (o.C + AO_WAVES - 1) / AO_WAVES;
+    p->u = per <= 4 ? 4 : 8;
     p->shm = ((size_t)at.nq * at.hd + AO_WAVES * 64 + (size_t)na * 32 + (size_t)na * G * at.hd) * sizeof(float);
     return p->shm <= 64 * 1024;
 }
@@ -220,8 +285,13 @@ bool ao_plan(int fmt, const AttnArgs& at, const GemvArgs& o, AoPlan* p) {
 template <int HD, int G>
 hipError_t launch_hg(const AttnArgs& at, const GemvArgs& o, const AoPlan& p, hipStream_t st) {
     const dim3 grid((o.n_pad + 63) / 64), block(64 * AO_WAVES);
-    if (p.u == 4) launch_kernel((k_attn_o<HD, G, 4>), grid, block, p.shm, st, at, o, p.nwh);
-    else launch_kernel((k_attn_o<HD, G, 8>), grid, block, p.shm, st, at, o, p.nwh);
+    if (p.pre) {
+        if (p.u == 4) launch_kernel((k_attn_o<HD, G, 4, true>), grid, block, p.shm, st, at, o, p.nwh);
+        else launch_kernel((k_attn_o<HD, G, 8, true>), grid, block, p.shm, st, at, o, p.nwh);
+    } else {
+        if (p.u == 4) launch_kernel((k_attn_o<HD, G, 4, false>), grid, block, p.shm, st, at, o, p.nwh);
+        else launch_kernel((k_attn_o<HD, G, 8, false>), grid, block, p.shm, st, at, o, p.nwh);
+    }
     return hipGetLastError();
 }
 
