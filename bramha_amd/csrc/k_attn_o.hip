@@ -74,7 +74,7 @@ __global__ void __launch_bounds__(64 * AO_WAVES) k_attn_o(const AttnArgs at, con
     extern __shared__ float smem[];
     const int na = at.nkv * nwh;          // attention waves
     float* xs = smem;                     // [nq * HD] attention output
-    float* comb = xs + at.nq * HD;        // [NW][64] partial sums, then epilogue scratch
+    float* comb = xs + at.nq * HD;        // [NW][64] partial sums
     float* w_m = comb + NW * 64;          // [na][16] per-wave running maxima
     float* w_l = w_m + na * 16;           // [na][16] per-wave sums
     float* w_o = w_l + na * 16;           // [na][G][HD] per-wave unnormalised outputs
@@ -240,13 +240,23 @@ __global__ void __launch_bounds__(64 * AO_WAVES) k_attn_o(const AttnArgs at, con
     }
     comb[wave * 64 + lane] = acc;
     __syncthreads();
-    if (threadIdx.x < 64) {
-        float sum = comb[threadIdx.x];
-        for (int w = 1; w < NW; ++w) sum += comb[w * 64 + threadIdx.x];
-        comb[threadIdx.x] = sum;
+    // wave 0 (lane r finishes row tile * 64 + r, whose epilogue operands it loaded): the partial
+    // sums in wave order, then run_epilogue's batch-1 EPI_RESNORM arithmetic (x += acc + bias,
+    // xw = x * w_next, the tile's sum of squares) kept in registers instead of an LDS round trip
+    if (wave == 0) {
+        float sum = comb[lane];
+        for (int w = 1; w < NW; ++w) sum += comb[w * 64 + lane];
+        const int64_t nn = (int64_t)tile * 64 + lane;
+        float sq = 0.f;
+        if (nn < a.N) {
+            const float v = pre.x0 + (sum * row_scale<BH_Q4_G32>(a.S, nn) + pre.bias);
+            a.y[nn] = v;
+            a.xw_out[nn] = v * pre.w1;
+            sq = v * v;
+        }
+        const float t = wave_sum64(sq);
+        if (lane == 0 && tile < a.ssq_tiles) a.ssq_out[tile] = t;
     }
-    __syncthreads();
-    run_epilogue<BH_Q4_G32, 1, EPI_RESNORM, 64>(a, comb, comb + 64, comb, (int64_t)tile * 64, &pre);
 }
 
 struct AoPlan {

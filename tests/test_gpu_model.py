@@ -118,6 +118,19 @@ def test_tiny_sink_eviction(plane):
     assert np.max(np.abs(olg - glg)) <= 1e-4 * max(1.0, np.abs(olg).max())
 
 
+def test_tiny_fp16_kv_sink_eviction_o_bias(plane):
+    """Batch-1 decode over an fp16 cache (attention, O projection and residual add in one
+    launch) with sink eviction (a 16-row ring after 4 sink rows) and an O bias."""
+    cfg = tiny_cfg(Q4_G32, Q4_G32, gqa7=True, kv_f16=True, max_context=16, sink_tokens=4, o_bias=True)
+    om, gm = _pair(plane, cfg, seed=45)
+    p = prompt(6, cfg.vocab, seed=46)
+    oids, olg = om.generate(p, 30, want_logits=True)  # rows pass 16 at step 11
+    gids, glg = gm.generate(p, 30, want_logits=True)
+    n = _margin_ok(oids, gids, olg, glg)
+    assert n >= 12
+    assert np.max(np.abs(olg[:n] - glg[:n])) < 2e-2 and max(rel_l2(glg[t], olg[t]) for t in range(n)) < 1e-3
+
+
 def test_tiny_fp16_kv(plane):
     cfg = tiny_cfg(Q4_G32, Q4_G32, gqa7=True, kv_f16=True)
     om, gm = _pair(plane, cfg, seed=7)
