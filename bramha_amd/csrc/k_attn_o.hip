@@ -241,21 +241,11 @@ __global__ void __launch_bounds__(64 * AO_WAVES) k_attn_o(const AttnArgs at, con
     comb[wave * 64 + lane] = acc;
     __syncthreads();
     // wave 0 (lane r finishes row tile * 64 + r, whose epilogue operands it loaded): the partial
-    // sums in wave order, then run_epilogue's batch-1 EPI_RESNORM arithmetic (x += acc + bias,
-    // xw = x * w_next, the tile's sum of squares) kept in registers instead of an LDS round trip
+    // sums in wave order, then the residual epilogue in registers
     if (wave == 0) {
         float sum = comb[lane];
         for (int w = 1; w < NW; ++w) sum += comb[w * 64 + lane];
-        const int64_t nn = (int64_t)tile * 64 + lane;
-        float sq = 0.f;
-        if (nn < a.N) {
-            const float v = pre.x0 + (sum * row_scale<BH_Q4_G32>(a.S, nn) + pre.bias);
-            a.y[nn] = v;
-            a.xw_out[nn] = v * pre.w1;
-            sq = v * v;
-        }
-        const float t = wave_sum64(sq);
-        if (lane == 0 && tile < a.ssq_tiles) a.ssq_out[tile] = t;
+        resnorm_wave<BH_Q4_G32>(a, sum, (int64_t)tile * 64, pre);
     }
 }
 

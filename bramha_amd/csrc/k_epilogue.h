@@ -172,6 +172,47 @@ __device__ __forceinline__ bool split_reduce(const GemvArgs& a, float* comb, int
     return true;
 }
 
+// split_reduce for one wave holding the tile's 64 sums (batch 1, lane = row): the same pairs
+// published, the same arrival count and the same split-order sum, with the pairs gathered by
+// cross-lane reads instead of LDS and barriers. Returns false where another workgroup finishes
+// the tile; on true, `sum` holds the lane's total.
+__device__ __forceinline__ bool split_reduce_wave(const GemvArgs& a, float& sum, int tile, int kws) {
+    constexpr int TOT = 64;
+    const int lane = threadIdx.x & 63;
+    const int ksw = a.ksw;
+    const float e0 = __shfl(sum, (2 * lane) & 63), e1 = __shfl(sum, (2 * lane + 1) & 63);
+    float* mine = a.part + (int64_t)(tile * ksw + kws) * TOT;
+    unsigned long long sink = 0;
+    if (lane < TOT / 2) {
+        const unsigned long long v = (unsigned long long)__float_as_uint(e0) | ((unsigned long long)__float_as_uint(e1) << 32);
+        sink = __hip_atomic_exchange((unsigned long long*)&mine[2 * lane], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    asm volatile("" ::"v"(sink));  // the wave's exchanges have completed before the count
+    int last = 0;
+    if (lane == 0)
+        last = __hip_atomic_fetch_add(&a.tile_cnt[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ksw - 1;
+    if (!__shfl(last, 0)) return false;
+    const float* all = a.part + (int64_t)tile * ksw * TOT;
+    float s0 = 0.f, s1 = 0.f;
+    if (lane < TOT / 2) {
+        unsigned long long v[MAX_KSW];
+#pragma unroll
+        for (int k = 0; k < MAX_KSW; ++k)
+            v[k] = __hip_atomic_load((const unsigned long long*)&all[(int64_t)min(k, ksw - 1) * TOT + 2 * lane],
+                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int k = 0; k < MAX_KSW; ++k) {
+            s0 += k < ksw ? __uint_as_float((unsigned)v[k]) : 0.f;
+            s1 += k < ksw ? __uint_as_float((unsigned)(v[k] >> 32)) : 0.f;
+        }
+    }
+    // element 2k + j is s_j of lane k
+    const float t0 = __shfl(s0, lane >> 1), t1 = __shfl(s1, lane >> 1);
+    sum = (lane & 1) ? t1 : t0;
+    if (lane == 0) __hip_atomic_store(&a.tile_cnt[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+}
+
 // LM-head element of token b, row nn: the raw logit is stored, then the repetition penalty
 // (cpu_engine.rs:2984-2992) applied `cnt` times; -inf for rows past the vocabulary, tokens past
 // the batch and NaN (the first-max scan uses `>`, so NaN never wins).
@@ -289,6 +330,25 @@ struct EpiPre {
         }
     }
 };
+
+// run_epilogue's batch-1 EPI_RESNORM for one 64-row tile finished by one wave whose lane r
+// holds row row0 + r's sum (and loaded its operands into `pre`): x += acc + bias, xw = x * w_next,
+// the tile's sum of squares, all in registers.
+template <int FMT>
+__device__ __forceinline__ void resnorm_wave(const GemvArgs& a, float sum, int64_t row0, const EpiPre<EPI_RESNORM>& pre) {
+    const int lane = threadIdx.x & 63;
+    const int64_t nn = row0 + lane;
+    float sq = 0.f;
+    if (nn < a.N) {
+        const float v = pre.x0 + (sum * row_scale<FMT>(a.S, nn) + pre.bias);
+        a.y[nn] = v;
+        a.xw_out[nn] = v * pre.w1;
+        sq = v * v;
+    }
+    const float t = wave_sum64(sq);
+    const int64_t tile = row0 / 64;
+    if (lane == 0 && tile < a.ssq_tiles) a.ssq_out[tile] = t;
+}
 
 template <int FMT, int B, int EPI, int ROWS>
 __device__ __forceinline__ void run_epilogue(const GemvArgs& a, const float* fin, float* scratch, const float* rn,

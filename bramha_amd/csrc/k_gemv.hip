@@ -74,6 +74,19 @@ __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
         touch_sink<B>(touch);
     }
 
+    if constexpr (B == 1 && EPI == EPI_RESNORM && RW == 1) {
+        // batch-1 residual producer: wave 0 (lane = row, holding the row's epilogue operands)
+        // sums the waves' partials in order, reduces the K split and finishes the tile in
+        // registers; the other waves are done
+        __syncthreads();
+        if (wave != 0) return;
+        float sum = comb[lane];
+        for (int w = 1; w < ksplit; ++w) sum += comb[w * TOT + lane];
+        if (ksw > 1 && !split_reduce_wave(a, sum, tile, kws)) return;
+        resnorm_wave<FMT>(a, sum, (int64_t)tile * ROWS, pre);
+        return;
+    }
+
     // ---- combine the K-split partial sums in a fixed order ----
     __syncthreads();
     for (int i = threadIdx.x; i < TOT; i += blockDim.x) {
