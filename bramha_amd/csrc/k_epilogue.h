@@ -350,35 +350,65 @@ __device__ __forceinline__ void resnorm_wave(const GemvArgs& a, float sum, int64
     if (lane == 0 && tile < a.ssq_tiles) a.ssq_out[tile] = t;
 }
 
+// Row offset of row nn's rotate-half RoPE partner (+- hd/2 within its head).
+__device__ __forceinline__ int qkv_partner(const GemvArgs& a, int64_t nn) {
+    const int sec = nn < a.qd ? 0 : (nn < a.qd + a.kd ? 1 : 2);
+    const int loc = (int)nn - (sec == 0 ? 0 : (sec == 1 ? a.qd : a.qd + a.kd));
+    return loc % a.hd < (a.hd >> 1) ? (a.hd >> 1) : -(a.hd >> 1);
+}
+
+// Batch-1 EPI_QKV for row nn < N: its sum and its RoPE partner's (rn0 the token's norm factor,
+// operands in `pre`): bias, rotate-half RoPE (apply_rope_cpu, cpu_engine.rs:1682-1699), q to y,
+// k and v to the KV cache.
+template <int FMT>
+__device__ __forceinline__ void qkv_row(const GemvArgs& a, int64_t nn, float sum, float psum, float rn0,
+                                        const EpiPre<EPI_QKV>& pre) {
+    const int half = a.hd >> 1;
+    const int sec = nn < a.qd ? 0 : (nn < a.qd + a.kd ? 1 : 2);
+    const int loc = (int)nn - (sec == 0 ? 0 : (sec == 1 ? a.qd : a.qd + a.kd));
+    const int hh = loc / a.hd, d = loc % a.hd;
+    float val = sum * row_scale<FMT>(a.S, nn) * rn0 + pre.bias;
+    if (sec < 2) {
+        const int dp = d < half ? half : -half;
+        const float pv = psum * row_scale<FMT>(a.S, nn + dp) * rn0 + pre.pbias;
+        val = d < half ? (val * pre.cs.x - pv * pre.cs.y) : (val * pre.cs.x + pv * pre.cs.y);
+    }
+    if (sec == 0) {
+        a.y[nn] = val;
+    } else {
+        const int64_t head = (int64_t)hh * a.kv.kv_rows * a.hd;
+        if (a.kv.kv_f16) {
+            if (sec == 1) ((__half*)a.kv.k)[head + kv_k_off(pre.kvrow, d, a.hd)] = __float2half(val);
+            else ((__half*)a.kv.v)[head + kv_v_off(pre.kvrow, d, a.hd)] = __float2half(val);
+        } else {
+            ((float*)(sec == 1 ? a.kv.k : a.kv.v))[head + pre.kvrow * a.hd + d] = val;
+        }
+    }
+}
+
+// Batch-1 EPI_QKV for one 64-row tile finished by one wave (lane r = row row0 + r, holding its
+// sum and operands): the partner's sum is read from lane r +- hd/2 (heads never straddle a tile).
+template <int FMT>
+__device__ __forceinline__ void qkv_wave(const GemvArgs& a, float sum, float rn0, int64_t row0, const EpiPre<EPI_QKV>& pre) {
+    const int lane = threadIdx.x & 63;
+    const int64_t nn = row0 + lane;
+    const float psum = __shfl(sum, (lane + qkv_partner(a, nn)) & 63);
+    if (nn < a.N) qkv_row<FMT>(a, nn, sum, psum, rn0, pre);
+}
+
 template <int FMT, int B, int EPI, int ROWS>
 __device__ __forceinline__ void run_epilogue(const GemvArgs& a, const float* fin, float* scratch, const float* rn,
                                              int64_t row0, const EpiPre<EPI>* pre = nullptr) {
     if constexpr (B == 1) {
         if (pre) {  // batch 1 with prefetched operands: thread r finishes row row0 + r
-            const int lane = threadIdx.x & 63;
-            const int wave = threadIdx.x >> 6;
-            const int nwaves = blockDim.x >> 6;
             const int rr = threadIdx.x;
             const int64_t nn = row0 + rr;
             const bool ok = rr < ROWS && nn < a.N;
             if constexpr (EPI == EPI_STORE) {
                 if (ok) a.y[nn] = fin[rr] * row_scale<FMT>(a.S, nn) * rn[0] + pre->bias;
             } else if constexpr (EPI == EPI_RESNORM) {
-                float sq = 0.f;
-                if (ok) {
-                    const float v = pre->x0 + (fin[rr] * row_scale<FMT>(a.S, nn) + pre->bias);
-                    a.y[nn] = v;
-                    a.xw_out[nn] = v * pre->w1;
-                    sq = v * v;
-                }
-                if (rr < ROWS) scratch[rr] = sq;
-                __syncthreads();
-                constexpr int SUB = ROWS / 64;
-                for (int q = wave; q < SUB; q += nwaves) {
-                    const float t = wave_sum64(scratch[q * 64 + lane]);
-                    const int64_t tile = row0 / 64 + q;
-                    if (lane == 0 && tile < a.ssq_tiles) a.ssq_out[tile] = t;
-                }
+                static_assert(ROWS == 64, "one wave finishes a 64-row tile");
+                if (threadIdx.x < 64) resnorm_wave<FMT>(a, fin[threadIdx.x], row0, *pre);
             } else if constexpr (EPI == EPI_SILU) {
                 if (ok) {
                     const float g = fin[rr] * row_scale<FMT>(a.S, nn) * rn[0];
@@ -386,29 +416,7 @@ __device__ __forceinline__ void run_epilogue(const GemvArgs& a, const float* fin
                     a.y[nn] = g * (1.0f / (1.0f + expf(-g))) * u;
                 }
             } else if constexpr (EPI == EPI_QKV) {
-                if (ok) {
-                    const int half = a.hd >> 1;
-                    float val = fin[rr] * row_scale<FMT>(a.S, nn) * rn[0] + pre->bias;
-                    const int sec = nn < a.qd ? 0 : (nn < a.qd + a.kd ? 1 : 2);
-                    const int loc = (int)nn - (sec == 0 ? 0 : (sec == 1 ? a.qd : a.qd + a.kd));
-                    const int hh = loc / a.hd, d = loc % a.hd;
-                    if (sec < 2) {  // rotate-half RoPE (apply_rope_cpu, cpu_engine.rs:1682-1699)
-                        const int dp = d < half ? half : -half;
-                        const float pv = fin[rr + dp] * row_scale<FMT>(a.S, nn + dp) * rn[0] + pre->pbias;
-                        val = d < half ? (val * pre->cs.x - pv * pre->cs.y) : (val * pre->cs.x + pv * pre->cs.y);
-                    }
-                    if (sec == 0) {
-                        a.y[nn] = val;
-                    } else {
-                        const int64_t head = (int64_t)hh * a.kv.kv_rows * a.hd;
-                        if (a.kv.kv_f16) {
-                            if (sec == 1) ((__half*)a.kv.k)[head + kv_k_off(pre->kvrow, d, a.hd)] = __float2half(val);
-                            else ((__half*)a.kv.v)[head + kv_v_off(pre->kvrow, d, a.hd)] = __float2half(val);
-                        } else {
-                            ((float*)(sec == 1 ? a.kv.k : a.kv.v))[head + pre->kvrow * a.hd + d] = val;
-                        }
-                    }
-                }
+                if (ok) qkv_row<FMT>(a, nn, fin[rr], fin[rr + qkv_partner(a, nn)], rn[0], *pre);
             } else if constexpr (EPI == EPI_LMHEAD) {
                 if (rr < ROWS) scratch[rr] = lm_elem<FMT>(a, fin[rr], 0, nn, rn, pre->cnt);
                 __syncthreads();

@@ -74,17 +74,24 @@ __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
         touch_sink<B>(touch);
     }
 
-    if constexpr (B == 1 && EPI == EPI_RESNORM && RW == 1) {
-        // batch-1 residual producer: wave 0 (lane = row, holding the row's epilogue operands)
-        // sums the waves' partials in order, reduces the K split and finishes the tile in
-        // registers; the other waves are done
-        __syncthreads();
-        if (wave != 0) return;
-        float sum = comb[lane];
-        for (int w = 1; w < ksplit; ++w) sum += comb[w * TOT + lane];
-        if (ksw > 1 && !split_reduce_wave(a, sum, tile, kws)) return;
-        resnorm_wave<FMT>(a, sum, (int64_t)tile * ROWS, pre);
-        return;
+    if constexpr (B == 1 && RW == 1 && (EPI == EPI_RESNORM || EPI == EPI_QKV)) {
+        // batch 1: wave 0 (lane = row, holding the row's epilogue operands) sums the waves'
+        // partials in order, reduces a residual producer's K split and finishes the tile in
+        // registers; the other waves are done. (The gate/up pair stays on the shared path: one
+        // wave summing both halves ran 0.5 % slower per step than two waves and a barrier.)
+        if (EPI == EPI_RESNORM || ksw == 1) {
+            __syncthreads();
+            if (wave != 0) return;
+            float sum = comb[lane];
+            for (int w = 1; w < ksplit; ++w) sum += comb[w * TOT + lane];
+            if constexpr (EPI == EPI_RESNORM) {
+                if (ksw > 1 && !split_reduce_wave(a, sum, tile, kws)) return;
+                resnorm_wave<FMT>(a, sum, (int64_t)tile * ROWS, pre);
+            } else {
+                qkv_wave<FMT>(a, sum, rn[0], (int64_t)tile * ROWS, pre);
+            }
+            return;
+        }
     }
 
     // ---- combine the K-split partial sums in a fixed order ----
