@@ -32,12 +32,18 @@ struct MfStage {
     uint4 x[S][TB][2];       // f32 activations of token tb * 16 + lr, k = 8 lg .. + 7
 };
 
+// blockIdx.y: token group, tokens blockIdx.y * B .. + B - 1 of the launch's arguments (a pass
+// of 32 tokens can run as two groups of 16: twice the workgroups, nothing shared between them),
+// each group with its own region of the split scratch.
 template <int FMT, int B, int EPI, int RW, int KW, int S>
-__global__ void __launch_bounds__(64 * KW * RW) k_gemm_mf(const GemvArgs a) {
+__global__ void __launch_bounds__(64 * KW * RW) k_gemm_mf(const GemvArgs a0) {
     constexpr int NACC = EPI == EPI_SILU ? 2 : 1;
     constexpr int ROWS = 64 * RW;
     constexpr int TB = B / 16;
     constexpr int TOT = NACC * B * ROWS;
+    GemvArgs a = gemv_tokens(a0, (int)blockIdx.y * B, B);
+    if (a0.part) a.part = a0.part + (int64_t)blockIdx.y * gridDim.x * TOT;
+    if (a0.tile_cnt) a.tile_cnt = a0.tile_cnt + blockIdx.y * (gridDim.x / a0.ksw);
     // S: chunks per pipeline stage (two stages in flight)
     extern __shared__ float smem[];
     float* rn = smem;          // [32] per-token norm factors
@@ -224,37 +230,38 @@ __global__ void __launch_bounds__(64 * KW * RW) k_gemm_mf(const GemvArgs a) {
 // ones, where occupancy decides (the 151936-row LM head at 32 tokens: 66 us with 4, 103 with 8).
 // One chunk per stage: two-chunk stages measured slower at every shape.
 template <int FMT, int B, int EPI, int RW, int KW>
-hipError_t launch_k(const GemvArgs& a, hipStream_t st) {
+hipError_t launch_k(const GemvArgs& a, int groups, hipStream_t st) {
     constexpr int NACC = EPI == EPI_SILU ? 2 : 1;
     constexpr int ROWS = 64 * RW;
     const int tiles = (a.n_pad + ROWS - 1) / ROWS;
     const size_t shm = (32 + (size_t)NACC * B * ROWS + (size_t)std::max(1, KW / 2) * B * (ROWS + 4)) * sizeof(float);
     if (shm > 64 * 1024) return hipErrorInvalidValue;
-    launch_kernel((k_gemm_mf<FMT, B, EPI, RW, KW, 1>), dim3(tiles * a.ksw), dim3(64 * KW * RW), shm, st, a);
+    launch_kernel((k_gemm_mf<FMT, B, EPI, RW, KW, 1>), dim3(tiles * a.ksw, groups), dim3(64 * KW * RW), shm, st, a);
     return hipGetLastError();
 }
 
 template <int FMT, int B, int EPI, int RW>
-hipError_t launch_t(const GemvArgs& a, hipStream_t st) {
+hipError_t launch_t(const GemvArgs& a, int groups, hipStream_t st) {
     if constexpr (RW == 1)
-        if ((a.n_pad + 63) / 64 * a.ksw <= 512) return launch_k<FMT, B, EPI, RW, 8>(a, st);
-    return launch_k<FMT, B, EPI, RW, 4>(a, st);
+        if ((a.n_pad + 63) / 64 * a.ksw * groups <= 512) return launch_k<FMT, B, EPI, RW, 8>(a, groups, st);
+    return launch_k<FMT, B, EPI, RW, 4>(a, groups, st);
 }
 
 template <int FMT, int EPI, int RW>
-hipError_t launch_b(const GemvArgs& a, int B, hipStream_t st) {
-    return B == 32 ? launch_t<FMT, 32, EPI, RW>(a, st) : launch_t<FMT, 16, EPI, RW>(a, st);
+hipError_t launch_b(const GemvArgs& a, int B, int groups, hipStream_t st) {
+    return B == 32 ? launch_t<FMT, 32, EPI, RW>(a, groups, st) : launch_t<FMT, 16, EPI, RW>(a, groups, st);
 }
 
 template <int FMT>
-hipError_t launch_e(int epi, const GemvArgs& a, int B, int rw, hipStream_t st) {
+hipError_t launch_e(int epi, const GemvArgs& a, int B, int groups, int rw, hipStream_t st) {
     switch (epi) {
-        case EPI_STORE: return launch_b<FMT, EPI_STORE, 1>(a, B, st);
-        case EPI_RESNORM: return launch_b<FMT, EPI_RESNORM, 1>(a, B, st);
-        case EPI_SILU: return launch_b<FMT, EPI_SILU, 1>(a, B, st);
-        case EPI_QKV: return rw == 2 ? launch_b<FMT, EPI_QKV, 2>(a, B, st) : launch_b<FMT, EPI_QKV, 1>(a, B, st);
+        case EPI_STORE: return launch_b<FMT, EPI_STORE, 1>(a, B, groups, st);
+        case EPI_RESNORM: return launch_b<FMT, EPI_RESNORM, 1>(a, B, groups, st);
+        case EPI_SILU: return launch_b<FMT, EPI_SILU, 1>(a, B, groups, st);
+        case EPI_QKV:
+            return rw == 2 ? launch_b<FMT, EPI_QKV, 2>(a, B, groups, st) : launch_b<FMT, EPI_QKV, 1>(a, B, groups, st);
         case EPI_LMHEAD:
-            if constexpr (FMT == BH_Q4_G32) return launch_b<FMT, EPI_LMHEAD, 1>(a, B, st);
+            if constexpr (FMT == BH_Q4_G32) return launch_b<FMT, EPI_LMHEAD, 1>(a, B, groups, st);
             return hipErrorInvalidValue;
         default: return hipErrorInvalidValue;
     }
@@ -264,8 +271,20 @@ hipError_t launch_e(int epi, const GemvArgs& a, int B, int rw, hipStream_t st) {
 
 hipError_t launch_gemm_mf(int fmt, int epi, const GemvArgs& a, int B, int rw, hipStream_t st) {
     if ((B != 16 && B != 32) || a.batch != B || a.ksw < 1 || a.n_pad % 64 || rw < 1 || rw > 2) return hipErrorInvalidValue;
-    if (fmt == BH_Q4_G32) return launch_e<BH_Q4_G32>(epi, a, B, rw, st);
-    if (fmt == BH_Q4_ROW) return launch_e<BH_Q4_ROW>(epi, a, B, rw, st);
+    // A 32-token pass whose launch leaves most CUs idle runs as two 16-token groups: twice the
+    // workgroups with no reduction between them (a 16-token pass of 896 x 896 takes 7.7 us, a
+    // 32-token one 10.2). Not for the LM head, whose row tiles fill the chip and whose weights
+    // the second group would stream again. Each group takes its own split scratch region.
+    int groups = 1;
+    const int tiles = (a.n_pad + 64 * rw - 1) / (64 * rw);
+    const int tot16 = (epi == EPI_SILU ? 2 : 1) * 16 * 64 * rw;
+    if (B == 32 && epi != EPI_LMHEAD && 2 * tiles * a.ksw <= 512 &&
+        (a.ksw == 1 || (2 * tiles <= SPLIT_WG_MAX && (int64_t)2 * tiles * a.ksw * tot16 <= (int64_t)SPLIT_WG_MAX * SPLIT_TOT_MAX))) {
+        groups = 2;
+        B = 16;
+    }
+    if (fmt == BH_Q4_G32) return launch_e<BH_Q4_G32>(epi, a, B, groups, rw, st);
+    if (fmt == BH_Q4_ROW) return launch_e<BH_Q4_ROW>(epi, a, B, groups, rw, st);
     return hipErrorInvalidValue;
 }
 
