@@ -108,6 +108,25 @@ def test_batch_decode_large_vocab(plane, nseq):
         assert np.max(np.abs(lg[:n, s] - wl)) <= 1e-4 * max(1.0, np.abs(wl).max()), s
 
 
+def test_batch32_token_groups_with_k_split(plane):
+    """32 sequences decoded together: every 32-token MFMA pass runs as two 16-token workgroup
+    groups; the down projection (FFN 2048: 64 chunks of K) also splits K over 4 workgroups per
+    row tile, each group with its own partial-sum and arrival-counter region."""
+    cfg = tiny_cfg(Q4_G32, Q4_G32, gqa7=True, ffn=2048, max_seqs=32, kv_rows=32 * 64)
+    om, gm = _pair(plane, cfg, seed=51)
+    prompts = [prompt(2 + (s * 3) % 17, cfg.vocab, seed=300 + s) for s in range(32)]
+    for s, p in enumerate(prompts):
+        gm.seq_open(s, 64)
+        gm.prefill(s, p[:-1])
+    gm.decode_setup(list(range(32)), [p[-1] for p in prompts])
+    ids, lg = gm.decode(6, want_logits=True)
+    for s, p in enumerate(prompts):
+        want, wl = om.generate(p, 6, want_logits=True)
+        n = len(want)
+        assert np.array_equal(ids[:n, s], want), s
+        assert np.max(np.abs(lg[:n, s] - wl)) <= 1e-4 * max(1.0, np.abs(wl).max()), s
+
+
 def test_tiny_sink_eviction(plane):
     cfg = tiny_cfg(F32, F32, max_context=16, sink_tokens=4)
     om, gm = _pair(plane, cfg, seed=5)
