@@ -22,7 +22,8 @@
 // they request and decode their weights to exact fp16 (q - 8) while the attention runs, and
 // after the merge spend one mixed-precision FMA per weight instead of the decode's 2.6 VALU
 // operations. fma(x, q - 8, p) scaled by s is fma(x, 16 (q - 8), p) scaled by s / 16 bit for bit
-// (power-of-two scaling commutes with rounding), so both variants compute k_gemv's values.
+// (power-of-two scaling commutes with rounding), so both variants evaluate every chunk exactly
+// as k_gemv does (the split of K over waves, and with it the order of the final sum, differs).
 //
 // Used when the projection needs no K split over workgroups (fewer than 64 chunks of K), for
 // Q4_G32 weights, an fp16 cache and contexts of at most 256 KiB of K and V.
