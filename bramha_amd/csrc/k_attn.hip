@@ -335,9 +335,11 @@ __global__ void __launch_bounds__(64 * NW) k_attn_mf(const AttnArgs a) {
                                (off & 63) == 0 && (a.kv.kv_rows & 7) == 0, ((off | a.kv.kv_rows) & 7) == 0,
                                r0, 0, 0, 0};
     aw.wv = wave;
-    // first tile requested before the sequence length is known, when it lies in the region
+    // first tile requested before the sequence length is known, when it lies in the region and
+    // in the split's rows (a tile past the split bound is never used)
     const int tfirst = r0 + wave * AttnWave<HD, NW, false>::TR;
-    const bool spec = a.static_off && aw.tiled && tfirst + AttnWave<HD, NW, false>::TR <= a.cap_rows;
+    const bool spec = a.static_off && aw.tiled && tfirst + AttnWave<HD, NW, false>::TR <= a.cap_rows &&
+                      tfirst < r0 + a.split_rows;
     if (spec) aw.load_full(aw.A, tfirst);
     int len;
     if (a.seq_len) {
