@@ -271,6 +271,63 @@ struct PenPre {
     }
 };
 
+// Batched residual-producer epilogue operands of the elements i = threadIdx.x + k * NT that a
+// thread finishes (token i / ROWS, row row0 + i % ROWS): the residual x, the next norm's
+// weight and the bias, requested at kernel start so that their latency hides under the weight
+// stream. Only the launch's own epilogue writes those x elements.
+template <int B, int ROWS, int NT>
+struct ResPre {
+    static constexpr int PER = (B * ROWS + NT - 1) / NT;
+    float x0[PER], w1[PER], bias[PER];
+    __device__ __forceinline__ void load(const GemvArgs& a, int64_t row0) {
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int i = threadIdx.x + k * NT;
+            const int b = i / ROWS;
+            const int64_t nn = row0 + i % ROWS;
+            x0[k] = w1[k] = bias[k] = 0.f;
+            if (i < B * ROWS && b < a.batch && nn < a.N) {
+                x0[k] = a.y[(int64_t)b * a.ldy + nn];
+                w1[k] = a.wnext[nn];
+                if (a.bias) bias[k] = a.bias[nn];
+            }
+        }
+    }
+};
+
+// run_epilogue's batched EPI_RESNORM with the operands of ResPre (same arithmetic and order).
+template <int FMT, int B, int ROWS, int NT>
+__device__ __forceinline__ void run_resnorm_pre(const GemvArgs& a, const float* fin, float* scratch, int64_t row0,
+                                                const ResPre<B, ROWS, NT>& rp) {
+    static_assert(ROWS % 64 == 0, "one sum of squares per 64-row tile");
+#pragma unroll
+    for (int k = 0; k < ResPre<B, ROWS, NT>::PER; ++k) {
+        const int i = threadIdx.x + k * NT;
+        if (i >= B * ROWS) continue;
+        const int b = i / ROWS;
+        const int64_t nn = row0 + i % ROWS;
+        float sq = 0.f;
+        if (nn < a.N && b < a.batch) {
+            float o = fin[i] * row_scale<FMT>(a.S, nn);
+            if (a.bias) o += rp.bias[k];
+            const float v = rp.x0[k] + o;
+            a.y[(int64_t)b * a.ldy + nn] = v;
+            a.xw_out[(int64_t)b * a.ldy + nn] = v * rp.w1[k];
+            sq = v * v;
+        }
+        scratch[i] = sq;
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int SUB = ROWS / 64;
+    for (int q = wave; q < B * SUB; q += NT / 64) {
+        const int b = q / SUB, sub = q % SUB;
+        const float t = wave_sum64(scratch[b * ROWS + sub * 64 + lane]);
+        const int64_t tile = row0 / 64 + sub;
+        if (lane == 0 && b < a.batch && tile < a.ssq_tiles) a.ssq_out[(int64_t)b * a.ssq_tiles + tile] = t;
+    }
+}
+
 // The batched LM-head epilogue with the counts of PenPre (run_epilogue's EPI_LMHEAD otherwise).
 template <int FMT, int B, int ROWS, int NT>
 __device__ __forceinline__ void run_lmhead_pre(const GemvArgs& a, const float* fin, float* scratch, const float* rn,

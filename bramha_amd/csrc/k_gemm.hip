@@ -152,6 +152,8 @@ __global__ void __launch_bounds__(64 * KW * RW) k_gemm_mf(const GemvArgs a0) {
     constexpr int NT = 64 * KW * RW;
     PenPre<B, ROWS, NT> pp;  // LM head: penalty counts, in flight with the weight stream
     if constexpr (EPI == EPI_LMHEAD) pp.load(a, (int64_t)tile * ROWS);
+    ResPre<B, ROWS, NT> rp;  // residual producers: residual, norm weight, bias, likewise
+    if constexpr (EPI == EPI_RESNORM) rp.load(a, (int64_t)tile * ROWS);
     if (c0 < c1) {
         for (int c = c0;; c += 2 * S) {
             fetch(c + S, s1);
@@ -221,6 +223,8 @@ __global__ void __launch_bounds__(64 * KW * RW) k_gemm_mf(const GemvArgs a0) {
     __syncthreads();
     if constexpr (EPI == EPI_LMHEAD)
         run_lmhead_pre<FMT, B, ROWS, NT>(a, comb, comb + TOT, rn, (int64_t)tile * ROWS, pp);
+    else if constexpr (EPI == EPI_RESNORM)
+        run_resnorm_pre<FMT, B, ROWS, NT>(a, comb, comb + TOT, (int64_t)tile * ROWS, rp);
     else
         run_epilogue<FMT, B, EPI, ROWS>(a, comb, comb + TOT, rn, (int64_t)tile * ROWS);
 }
