@@ -344,7 +344,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU: the decode path runs on a single MI355X "
-              "(--gpus %d requested). Multi-GPU sharding is described in DESIGN.md, not run." % args.gpus,
+              "(--gpus %d requested); sharding across GPUs is not implemented." % args.gpus,
               file=sys.stderr)
         sys.exit(2)
 
