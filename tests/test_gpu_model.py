@@ -111,8 +111,9 @@ def test_batch_decode_large_vocab(plane, nseq):
 def test_batch32_token_groups_with_k_split(plane):
     """32 sequences decoded together: every 32-token MFMA pass runs as two 16-token workgroup
     groups; the down projection (FFN 2048: 64 chunks of K) also splits K over 4 workgroups per
-    row tile, each group with its own partial-sum and arrival-counter region."""
-    cfg = tiny_cfg(Q4_G32, Q4_G32, gqa7=True, ffn=2048, max_seqs=32, kv_rows=32 * 64)
+    row tile, each group with its own partial-sum and arrival-counter region. An O bias takes the
+    batched residual epilogue's prefetched bias."""
+    cfg = tiny_cfg(Q4_G32, Q4_G32, gqa7=True, ffn=2048, max_seqs=32, kv_rows=32 * 64, o_bias=True)
     om, gm = _pair(plane, cfg, seed=51)
     prompts = [prompt(2 + (s * 3) % 17, cfg.vocab, seed=300 + s) for s in range(32)]
     for s, p in enumerate(prompts):
@@ -230,16 +231,21 @@ def test_graph_replay_matches_single_steps(plane):
     assert np.array_equal(a, b) and np.array_equal(la, lb)
 
 
-@pytest.mark.parametrize("shape,plen", [("gqa7", 20), ("gqa7", 100), ("gqa7", 300), ("hd128", 40), ("hd128", 200)])
+@pytest.mark.parametrize("shape,plen", [("gqa7", 20), ("gqa7", 100), ("gqa7", 300), ("hd128", 40), ("hd128", 200),
+                                        ("g1", 40), ("g4", 100), ("g8", 40)])
 def test_batch1_attention_o_launch_matches_batched_path(plane, shape, plen):
     """Batch-1 decode over an fp16 cache computes attention, the O projection and the residual
     add in one launch; a batch of two runs them as separate kernels. The same prompt decoded
     both ways gives the same ids and logits to 1e-4 (the launches differ only in summation
     order). Context bounds of 64, 128 and 512 rows (one tile per attention wave at 1, 2 and 8
     waves per KV head); head_dim 128 with two KV heads at bounds of 64 (2 waves of one tile)
-    and 256 rows (4 waves of two tiles)."""
+    and 256 rows (4 waves of two tiles); 1, 4 and 8 query heads per KV head."""
     if shape == "hd128":
         cfg = tiny_cfg(Q4_G32, Q4_G32, kv_f16=True, hidden=512, n_heads=4, n_kv_heads=2, head_dim=128, ffn=768)
+    elif shape in ("g1", "g4", "g8"):
+        heads = {"g1": (4, 4), "g4": (4, 1), "g8": (8, 1)}[shape]
+        cfg = tiny_cfg(Q4_G32, Q4_G32, kv_f16=True, hidden=64 * heads[0], n_heads=heads[0], n_kv_heads=heads[1],
+                       head_dim=64, ffn=512, vocab=1024)
     else:
         cfg = tiny_cfg(Q4_G32, Q4_G32, gqa7=True, kv_f16=True)
     _, gm = _pair(plane, cfg, seed=41)
