@@ -88,10 +88,17 @@ def roofline(m, n_steps=16, traffic=False):
     mean_us = t[best][0]
     nbytes = m.kernel_bytes(best)
     achieved = nbytes / (mean_us * 1e-6)
+    # the step's weight-streaming launch (the LM head), measured the same way, for comparison
+    lm_us = t["lm_head"][0]
+    lm_bytes = m.kernel_bytes("lm_head")
+    stream = {"kernel": "lm_head", "mean_us": lm_us, "bytes_per_launch": lm_bytes,
+              "achieved": lm_bytes / (lm_us * 1e-6) / 1e9 if lm_us else None,
+              "frac": lm_bytes / (lm_us * 1e-6) / HBM_PEAK if lm_us else None}
     return best, {"bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                   "frac": achieved / HBM_PEAK, "traffic": pmc_traffic(best) if traffic else None, "kernel": best,
                   "bytes_per_launch": nbytes,
                   "mean_us": mean_us,
+                  "weight_stream": stream,
                   "per_class_us": {k: round(v[0], 3) for k, v in t.items()},
                   "launches_per_step": {k: v[1] // n_steps for k, v in t.items()}}
 
