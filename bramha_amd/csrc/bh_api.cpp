@@ -90,6 +90,10 @@ int alloc_weight(bh_ctx* ctx, int fmt, int64_t n, int64_t k, DevWeight& w) {
     w.k = k;
     w.n_pad = pad64(n);
     w.chunks = k / E;
+    // the kernels address a weight with 32-bit buffer offsets
+    if (w.chunks * w.n_pad * 16 >= ((int64_t)1 << 31))
+        return ctx->fail(BH_ERR_UNSUPPORTED, "weight " + std::to_string(n) + "x" + std::to_string(k) +
+                                                 ": 2 GiB or more of packed data (the kernels use 32-bit offsets)");
     const size_t qb = (size_t)(w.chunks * w.n_pad * 16);
     size_t sb = 0;
     if (fmt == BH_Q4_G32) sb = (size_t)(w.chunks * w.n_pad * 2);
@@ -331,8 +335,12 @@ void bh_destroy(bh_ctx* ctx) {
     if (ctx->d_x) hipFree(ctx->d_x);
     if (ctx->d_y) hipFree(ctx->d_y);
     for (auto& kv : ctx->rope_tabs) hipFree(kv.second);
-    if (ctx->attn_part) hipFree(ctx->attn_part);
-    if (ctx->attn_cnt) hipFree(ctx->attn_cnt);
+    hipDeviceSynchronize();  // calls on the caller's streams used the attention scratch
+    for (auto& kv : ctx->attn_scratch) {
+        if (kv.second.part) hipFree(kv.second.part);
+        if (kv.second.cnt) hipFree(kv.second.cnt);
+    }
+    for (void* p : ctx->retired) hipFree(p);
     if (ctx->split_part) hipFree(ctx->split_part);
     if (ctx->split_cnt) hipFree(ctx->split_cnt);
     hipStreamDestroy(ctx->stream);
@@ -540,10 +548,10 @@ int bh_silu_mul(bh_ctx* ctx, const float* g, const float* u, float* out, int64_t
     return e == hipSuccess ? BH_OK : ctx->hip_fail(e, "silu launch");
 }
 
-// Attention arguments and the split scratch of bh_attn_decode (context lock held).
-static int attn_args(bh_ctx* ctx, const float* q, const void* k, const void* v, int kv_f16, int64_t kv_rows,
-                     const int64_t* seq_off, const int32_t* seq_len, int batch, int n_q, int n_kv, int head_dim,
-                     int max_len, float* out, AttnArgs& a) {
+// Attention arguments (everything but the split scratch).
+static void attn_fill(const float* q, const void* k, const void* v, int kv_f16, int64_t kv_rows, const int64_t* seq_off,
+                      const int32_t* seq_len, int batch, int n_q, int n_kv, int head_dim, int max_len, float* out,
+                      AttnArgs& a) {
     a.q = q;
     a.out = out;
     a.kv.k = (void*)k;
@@ -557,29 +565,47 @@ static int attn_args(bh_ctx* ctx, const float* q, const void* k, const void* v, 
     a.nkv = n_kv;
     a.hd = head_dim;
     attn_plan(std::max(max_len, 1), batch, n_kv, head_dim, &a.splits, &a.split_rows);
-    if (a.splits > 1) {
-        const size_t need = (size_t)batch * n_q * a.splits * (head_dim + 2) * 4;
-        if (need > ctx->attn_part_bytes) {
-            if (ctx->attn_part) hipFree(ctx->attn_part);
-            ctx->attn_part = nullptr;
-            ctx->attn_part_bytes = 0;
-            hipError_t e = hipMalloc(&ctx->attn_part, need);
-            if (e != hipSuccess) return ctx->hip_fail(e, "hipMalloc(attention partials)");
-            ctx->attn_part_bytes = need;
+}
+
+static bool capturing(hipStream_t st) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
+// Attention arguments and the split scratch of `st` for bh_attn_decode (context lock held).
+static int attn_args(bh_ctx* ctx, hipStream_t st, const float* q, const void* k, const void* v, int kv_f16,
+                     int64_t kv_rows, const int64_t* seq_off, const int32_t* seq_len, int batch, int n_q, int n_kv,
+                     int head_dim, int max_len, float* out, AttnArgs& a) {
+    attn_fill(q, k, v, kv_f16, kv_rows, seq_off, seq_len, batch, n_q, n_kv, head_dim, max_len, out, a);
+    if (a.splits <= 1) return BH_OK;
+    const size_t need = (size_t)batch * n_q * a.splits * (head_dim + 2) * 4;
+    const int need_cnt = batch * n_kv;
+    bh_ctx::AttnScratch& sc = ctx->attn_scratch[st];
+    if (need > sc.part_bytes || need_cnt > sc.cnt_len) {
+        if (capturing(st))
+            return ctx->fail(BH_ERR_CAPACITY, "attention split scratch of this stream is too small for a call made "
+                                              "under graph capture: make one uncaptured call of this size first");
+        // the old buffers stay allocated (a captured graph may hold them); in-flight work finishes
+        hipError_t e = hipStreamSynchronize(st);
+        if (e != hipSuccess) return ctx->hip_fail(e, "hipStreamSynchronize");
+        bh_ctx::AttnScratch ns;
+        ns.part_bytes = std::max(need, sc.part_bytes);
+        ns.cnt_len = std::max(need_cnt, sc.cnt_len);
+        e = hipMalloc(&ns.part, ns.part_bytes);
+        if (e == hipSuccess) e = hipMalloc((void**)&ns.cnt, (size_t)ns.cnt_len * 4);
+        if (e == hipSuccess) e = hipMemset(ns.cnt, 0, (size_t)ns.cnt_len * 4);
+        if (e != hipSuccess) {
+            if (ns.part) hipFree(ns.part);
+            if (ns.cnt) hipFree(ns.cnt);
+            return ctx->hip_fail(e, "hipMalloc(attention scratch)");
         }
-        a.part_o = (float*)ctx->attn_part;
-        a.part_ml = a.part_o + (size_t)batch * n_q * a.splits * head_dim;
-        if (batch * n_kv > ctx->attn_cnt_len) {
-            if (ctx->attn_cnt) hipFree(ctx->attn_cnt);
-            ctx->attn_cnt = nullptr;
-            ctx->attn_cnt_len = 0;
-            hipError_t e = hipMalloc((void**)&ctx->attn_cnt, (size_t)batch * n_kv * 4);
-            if (e == hipSuccess) e = hipMemset(ctx->attn_cnt, 0, (size_t)batch * n_kv * 4);
-            if (e != hipSuccess) return ctx->hip_fail(e, "hipMalloc(attention counters)");
-            ctx->attn_cnt_len = batch * n_kv;
-        }
-        a.cnt = ctx->attn_cnt;
+        if (sc.part) ctx->retired.push_back(sc.part);
+        if (sc.cnt) ctx->retired.push_back(sc.cnt);
+        sc = ns;
     }
+    a.part_o = (float*)sc.part;
+    a.part_ml = a.part_o + (size_t)batch * n_q * a.splits * head_dim;
+    a.cnt = sc.cnt;
     return BH_OK;
 }
 
@@ -603,10 +629,11 @@ int bh_attn_decode(bh_ctx* ctx, const float* q, const void* k, const void* v, in
     if (rc) return rc;
     if (batch == 0) return BH_OK;
     std::lock_guard<std::mutex> g(ctx->mu);
+    const hipStream_t st = pick(ctx, stream);
     AttnArgs a;
-    rc = attn_args(ctx, q, k, v, kv_f16, kv_rows, seq_off, seq_len, batch, n_q, n_kv, head_dim, max_len, out, a);
+    rc = attn_args(ctx, st, q, k, v, kv_f16, kv_rows, seq_off, seq_len, batch, n_q, n_kv, head_dim, max_len, out, a);
     if (rc) return rc;
-    hipError_t e = launch_attention(a, pick(ctx, stream));
+    hipError_t e = launch_attention(a, st);
     return e == hipSuccess ? BH_OK : ctx->hip_fail(e, "attention launch");
 }
 
@@ -703,7 +730,8 @@ int bh_time_attn(bh_ctx* ctx, const float* q, const void* k, const void* v, int 
     if (batch <= 0 || iters <= 0 || !us_per_launch) return BH_ERR_INVALID;
     std::lock_guard<std::mutex> g(ctx->mu);
     AttnArgs a;
-    rc = attn_args(ctx, q, k, v, kv_f16, kv_rows, seq_off, seq_len, batch, n_q, n_kv, head_dim, max_len, out, a);
+    rc = attn_args(ctx, ctx->stream, q, k, v, kv_f16, kv_rows, seq_off, seq_len, batch, n_q, n_kv, head_dim, max_len,
+                   out, a);
     if (rc) return rc;
     const size_t kvb = (size_t)kv_rows * n_kv * head_dim * (kv_f16 ? 2 : 4);
     const int copies = (int)std::max<size_t>(1, std::min<size_t>(256, (rotate_bytes + 2 * kvb - 1) / std::max<size_t>(2 * kvb, 1)));

@@ -31,10 +31,21 @@ struct bh_ctx {
     size_t x_cap = 0;
     void* d_y = nullptr;
     size_t y_cap = 0;
-    void* attn_part = nullptr;
-    size_t attn_part_bytes = 0;
-    int32_t* attn_cnt = nullptr;  // split-merge counters, zero when idle
-    int attn_cnt_len = 0;
+    // Split scratch of bh_attn_decode, one per stream it is called on (calls on one stream run in
+    // order, so they may share it): partials and split-merge counters (zero when idle). A buffer
+    // that grows is retired, not freed, while the context lives, since a graph captured from an
+    // earlier call may still write it.
+    struct AttnScratch {
+        void* part = nullptr;
+        size_t part_bytes = 0;
+        int32_t* cnt = nullptr;
+        int cnt_len = 0;
+    };
+    std::unordered_map<hipStream_t, AttnScratch> attn_scratch;
+    std::vector<void*> retired;
+    // This device's copy of the file-scope scratch of bh_attn_decode_noalloc (bh_api.cpp),
+    // resolved at bh_init.
+    uint8_t* noalloc_scratch = nullptr;
     std::unordered_map<std::string, void*> rope_tabs;
     // K-split scratch of the GEMVs launched on the context's own stream (split sums and arrival
     // counters, zero when idle); calls on other streams run unsplit so they never share it.

@@ -115,6 +115,11 @@ def quantize(fmt, w):
     return q, s
 
 
+def ragged_contexts(seed=0, n_seq=32, lo=128, hi=8192):
+    """Context lengths of the ragged batched-decode workload: n_seq draws uniform in [lo, hi]."""
+    return np.random.default_rng(seed).integers(lo, hi + 1, size=n_seq)
+
+
 def synth_weights(cfg, seed=0, sigma=0.02):
     """Random-init weights: matrices and biases N(0, sigma) from the named streams, norms 1.0.
     Yields (name, data, scales) in the formats the config names (scales None for f32)."""

@@ -6,7 +6,9 @@ last_accessed: u64 }`, stored as `<base>/prefix_kv_cache_data/<sha256(tokens as 
 for every prefix whose length is a multiple of 16 tokens; keys[layer] / values[layer] are the
 flat LayerKvCache rows [tokens][n_kv * head_dim] f32. Lookups try the longest page-aligned
 prefix first. `BRAMHA_PREFIX_CACHE=false` disables both directions and `BRAMHA_KV_TRIM_N`
-(default 4) trailing tokens are left out of what is saved, as in the reference.
+(default 4) trailing tokens are left out of what is saved, as in the reference. After each save
+the directory keeps its 20 most recently modified entries (PrefixCacheDb::enforce_limit,
+src/storage/cache_db.rs:9-34, called at prefix_cache.rs:162).
 
 The device side moves rows with bh_model_kv_read / bh_model_kv_write
 (HipDecoder.kv_read / kv_write); `prefill_cached` is the prefill flow of
@@ -14,6 +16,7 @@ generate_cpu_inner_logits with the cache (cpu_engine.rs:2518-2534, 2746-2756).
 """
 import hashlib
 import os
+import re
 import struct
 import time
 
@@ -21,6 +24,8 @@ import numpy as np
 
 PAGE_SIZE = 16  # prefix_cache.rs:44
 CACHE_DIR = "prefix_kv_cache_data"
+MAX_ENTRIES = 20  # prefix_cache.rs:162
+_USIZE_MAX = (1 << 64) - 1
 
 
 # ---- bincode standard configuration: little-endian, variable-length integers ----
@@ -98,6 +103,40 @@ def _now_ms():
     return int(time.time() * 1000)
 
 
+def _trim_n():
+    """BRAMHA_KV_TRIM_N as Rust's `parse::<usize>()` reads it (digits with an optional leading
+    '+', no sign, spaces or underscores, at most usize::MAX), else 4 (prefix_cache.rs:99-102)."""
+    v = os.environ.get("BRAMHA_KV_TRIM_N", "")
+    if not re.fullmatch(r"\+?[0-9]+", v):
+        return 4
+    n = int(v)
+    return n if n <= _USIZE_MAX else 4
+
+
+def enforce_limit(base_path, max_entries):
+    """Keep the max_entries most recently modified files of the cache directory and delete the
+    rest, oldest first (PrefixCacheDb::enforce_limit, cache_db.rs:9-34). Returns the number
+    deleted."""
+    cache_dir = os.path.join(base_path, CACHE_DIR)
+    if not os.path.isdir(cache_dir):
+        return 0
+    entries = []
+    for e in os.scandir(cache_dir):
+        if e.is_file():
+            entries.append((e.stat().st_mtime_ns, e.path))
+    if len(entries) <= max_entries:
+        return 0
+    entries.sort(key=lambda x: x[0])  # a stable sort by modification time, oldest first
+    gone = 0
+    for _, path in entries[:len(entries) - max_entries]:
+        try:
+            os.remove(path)
+            gone += 1
+        except OSError:
+            pass
+    return gone
+
+
 def find_longest_prefix(base_path, tokens):
     """(prefix_len, (tokens, keys, values, last_accessed)) of the longest cached page-aligned
     prefix of `tokens`, or None (prefix_cache.rs:37-80). A hit refreshes last_accessed."""
@@ -131,10 +170,7 @@ def save_prefix(base_path, tokens, keys, values):
         return
     tokens = np.asarray(tokens, dtype=np.uint32)
     n = len(tokens)
-    try:
-        trim = int(os.environ.get("BRAMHA_KV_TRIM_N", "4"))
-    except ValueError:
-        trim = 4
+    trim = _trim_n()
     if n <= trim:
         return
     active = n - trim
@@ -160,6 +196,7 @@ def save_prefix(base_path, tokens, keys, values):
             pv.append(v[:sl])
         with open(path, "wb") as f:
             f.write(encode_entry(tokens[:plen], pk, pv, _now_ms()))
+    enforce_limit(base_path, MAX_ENTRIES)
 
 
 def prefill_cached(model, slot, tokens, base_path):

@@ -66,7 +66,10 @@ _PROTOS = {
     "orc_model_destroy": (None, [_P]),
     "orc_model_set": (c_int, [_P, ctypes.c_char_p, _P, _P]),
     "orc_generate": (c_int64, [_P, _P, c_int64, c_int64, _P, _P]),
+    "orc_generate_ex": (c_int64, [_P, _P, c_int64, c_int64, _P, _P, c_int64, _P, _P, _P, _P, _P]),
     "orc_num_threads": (c_int, []),
+    "orc_set_threads": (None, [c_int]),
+    "orc_set_fast": (None, [c_int]),
 }
 for _n, (_r, _a) in _PROTOS.items():
     _f = getattr(_lib, _n)
@@ -239,6 +242,17 @@ def num_threads():
     return _lib.orc_num_threads()
 
 
+def set_threads(n):
+    """OpenMP thread count of the following oracle calls."""
+    _lib.orc_set_threads(int(n))
+
+
+def set_fast(on):
+    """True (default): the token-blocked / parallel loops; False: the scalar loops in the
+    reference's order that they are pinned against (bit-identical results)."""
+    _lib.orc_set_fast(1 if on else 0)
+
+
 class OracleModel:
     """The reference decode loop (generate_cpu_inner_logits, CPU-only, temperature 0)."""
 
@@ -278,4 +292,42 @@ class OracleModel:
         ids = np.empty(max(max_new, 1), np.uint32)
         lg = np.empty((max(max_new, 1), self.cfg.vocab), np.float32) if want_logits else None
         n = _lib.orc_generate(self.m, _p(p), p.size, max_new, _p(ids), _p(lg))
+        if n < 0:
+            raise ValueError("prefill past max_context with eviction (the reference's prefill attention "
+                             "indexes evicted rows and panics)")
         return (ids[:n].copy(), lg[:n].copy()) if want_logits else ids[:n].copy()
+
+    def generate_ex(self, prompt, max_new, want_logits=False, kv_in=None, want_kv=False):
+        """generate with a prefix-cache hit and/or the caches after the prefill.
+        kv_in: (k, v) arrays [n_layers][prefix_len][n_kv*head_dim] f32 holding the prompt's first
+        prefix_len rows (the prefill then starts at prefix_len). Returns (ids, logits or None,
+        (k, v) after the prefill or None)."""
+        c = self.cfg
+        kd = c.n_kv_heads * c.head_dim
+        p = np.ascontiguousarray(prompt, np.uint32)
+        ids = np.empty(max(max_new, 1), np.uint32)
+        lg = np.empty((max(max_new, 1), c.vocab), np.float32) if want_logits else None
+        plen, kin, vin = 0, None, None
+        if kv_in is not None:
+            kin = np.ascontiguousarray(kv_in[0], np.float32)
+            vin = np.ascontiguousarray(kv_in[1], np.float32)
+            plen = kin.shape[1]
+            assert kin.shape == vin.shape == (c.n_layers, plen, kd)
+        rows_cap = max(p.size - 1, 0)
+        if c.max_context > 0:
+            rows_cap = min(rows_cap, c.max_context)
+        rows_cap = max(rows_cap, plen)
+        # the library writes [n_layers][rows][kd] contiguously for the row count it reports
+        kout = np.empty(c.n_layers * rows_cap * kd, np.float32) if want_kv else None
+        vout = np.empty_like(kout) if want_kv else None
+        rows = c_int64(0)
+        n = _lib.orc_generate_ex(self.m, _p(p), p.size, max_new, _p(ids), _p(lg), plen, _p(kin), _p(vin),
+                                 _p(kout), _p(vout), ctypes.byref(rows))
+        if n < 0:
+            raise ValueError("prefill past max_context with eviction (the reference's prefill attention "
+                             "indexes evicted rows and panics)")
+        r = rows.value
+        assert r <= rows_cap
+        kv = (kout[:c.n_layers * r * kd].reshape(c.n_layers, r, kd).copy(),
+              vout[:c.n_layers * r * kd].reshape(c.n_layers, r, kd).copy()) if want_kv else None
+        return ids[:n].copy(), (lg[:n].copy() if want_logits else None), kv

@@ -203,8 +203,9 @@ void matvec_mul(const float* h, int64_t in_f, const WView& w, float* out, int64_
 }
 
 // gemm_cpu: cpu_engine.rs:565-708, the path taken whenever is_cpu (always, :573).
-// Single-threaded; F32/I8 single sum, U4 the 4-partial-sum order of a5.
-void gemm_cpu(const float* hb, const WView& w, int64_t bs, int64_t in_f, int64_t out_f, float* out) {
+// F32/I8 single sum, U4 the 4-partial-sum order of a5. The reference runs it on one thread;
+// this scalar form keeps its loop order, gemm_cpu below computes the same chains in parallel.
+void gemm_cpu_scalar(const float* hb, const WView& w, int64_t bs, int64_t in_f, int64_t out_f, float* out) {
     for (int64_t j = 0; j < out_f; ++j) {
         for (int64_t b = 0; b < bs; ++b) {
             const float* hr = hb + b * in_f;
@@ -235,6 +236,170 @@ void gemm_cpu(const float* hb, const WView& w, int64_t bs, int64_t in_f, int64_t
             }
         }
     }
+}
+
+// ---------------------------------------------------------------------------
+// Token-blocked forms for passes over many tokens (prefill). Every (token, row) output is
+// ONE sequential chain in exactly the order of the single-token function named beside it:
+// the tokens of a block only occupy separate SIMD lanes and the rows are spread over
+// threads, so no chain is split or reassociated and the results are bit-identical to the
+// scalar loops for any thread count. orc_set_fast(0) selects the scalar forms, against
+// which the tests pin these.
+// ---------------------------------------------------------------------------
+int g_fast = 1;
+constexpr int TB = 16;  // tokens per block
+
+// hT[i][t] = hb[b0 + t][i] for t < nb; zero in the padding lanes.
+void transpose_tokens(const float* hb, int64_t in_f, int64_t b0, int64_t nb, float* hT) {
+    for (int64_t i = 0; i < in_f; ++i)
+        for (int t = 0; t < TB; ++t) hT[i * TB + t] = t < nb ? hb[(b0 + t) * in_f + i] : 0.f;
+}
+
+// 8 float lanes (one AVX register). With -ffp-contract=off a * b + c stays a multiply and an add.
+typedef float v8 __attribute__((vector_size(32)));
+inline v8 ld8(const float* p) {
+    v8 r;
+    std::memcpy(&r, p, sizeof r);
+    return r;
+}
+inline void st8(float* p, v8 v) { std::memcpy(p, &v, sizeof v); }
+inline v8 bc8(float x) { return v8{x, x, x, x, x, x, x, x}; }
+
+// One row of matvec_mul's single running sum (matvec_row_single) for a block of tokens.
+inline void block_row_single(const float* hT, int64_t in_f, const WView& w, int64_t j, float* res) {
+    v8 a0 = bc8(0.f), a1 = bc8(0.f);
+    if (w.fmt == F32 || w.fmt == Q8_ROW) {
+        const float* wf = w.f + j * in_f;
+        const int8_t* w8 = w.q8 + j * in_f;
+        const bool f32 = w.fmt == F32;
+        for (int64_t i = 0; i < in_f; ++i) {
+            const v8 wi = bc8(f32 ? wf[i] : (float)w8[i]);
+            a0 += ld8(hT + i * TB) * wi;
+            a1 += ld8(hT + i * TB + 8) * wi;
+        }
+        if (!f32) {
+            a0 *= bc8(w.s[j]);
+            a1 *= bc8(w.s[j]);
+        }
+    } else {
+        const uint8_t* rb = w.q4 + j * (in_f / 2);
+        for (int64_t i = 0; i < in_f / 2; ++i) {
+            const v8 q1 = bc8(LUT.q1[rb[i]]), q2 = bc8(LUT.q2[rb[i]]);
+            const float* h0 = hT + (2 * i) * TB;
+            a0 += ld8(h0) * q1 + ld8(h0 + TB) * q2;
+            a1 += ld8(h0 + 8) * q1 + ld8(h0 + TB + 8) * q2;
+        }
+        a0 *= bc8(w.s[j]);
+        a1 *= bc8(w.s[j]);
+    }
+    st8(res, a0);
+    st8(res + 8, a1);
+}
+
+// The U4 order of a5 (four partial sums over the bytes of each 8-byte chunk, then the tail
+// bytes, then the row scale) for a block of tokens: gemm_cpu's and matvec_mul_into's Q4_ROW rows.
+inline void block_row_q4x4(const float* hT, int64_t in_f, const WView& w, int64_t j, float* res) {
+    const int64_t half_in = in_f / 2, chunks = half_in / 8;
+    const uint8_t* rb = w.q4 + j * half_in;
+    v8 s[4][2];
+    for (auto& x : s) x[0] = x[1] = bc8(0.f);
+    for (int64_t c = 0; c < chunks; ++c) {
+        for (int e = 0; e < 8; ++e) {
+            const uint8_t b = rb[c * 8 + e];
+            const v8 q1 = bc8(LUT.q1[b]), q2 = bc8(LUT.q2[b]);
+            const float* h0 = hT + (c * 16 + 2 * e) * TB;
+            s[e & 3][0] += ld8(h0) * q1 + ld8(h0 + TB) * q2;
+            s[e & 3][1] += ld8(h0 + 8) * q1 + ld8(h0 + TB + 8) * q2;
+        }
+    }
+    v8 sum0 = s[0][0] + s[1][0] + s[2][0] + s[3][0], sum1 = s[0][1] + s[1][1] + s[2][1] + s[3][1];
+    for (int64_t i = chunks * 8; i < half_in; ++i) {
+        const v8 q1 = bc8(LUT.q1[rb[i]]), q2 = bc8(LUT.q2[rb[i]]);
+        const float* h0 = hT + (2 * i) * TB;
+        sum0 += ld8(h0) * q1 + ld8(h0 + TB) * q2;
+        sum1 += ld8(h0 + 8) * q1 + ld8(h0 + TB + 8) * q2;
+    }
+    st8(res, sum0 * bc8(w.s[j]));
+    st8(res + 8, sum1 * bc8(w.s[j]));
+}
+
+// One row of matvec_mul_into (cpu_engine.rs:1311-1412) for a block of tokens: F32/I8 four
+// partial sums over stride-4 elements with the tail in s0, then (s0 + s1 + s2 + s3) (x scale).
+inline void block_row_into(const float* hT, int64_t in_f, const WView& w, int64_t j, float* res) {
+    if (w.fmt == Q4_ROW) {
+        block_row_q4x4(hT, in_f, w, j, res);
+        return;
+    }
+    const int64_t chunks = in_f / 4, rem = in_f % 4;
+    const float* wf = w.f + j * in_f;
+    const int8_t* w8 = w.q8 + j * in_f;
+    const bool f32 = w.fmt == F32;
+    v8 s[4][2];
+    for (auto& x : s) x[0] = x[1] = bc8(0.f);
+    for (int64_t c = 0; c < chunks; ++c) {
+        const int64_t b = c * 4;
+        for (int e = 0; e < 4; ++e) {
+            const v8 wi = bc8(f32 ? wf[b + e] : (float)w8[b + e]);
+            const float* h = hT + (b + e) * TB;
+            s[e][0] += ld8(h) * wi;
+            s[e][1] += ld8(h + 8) * wi;
+        }
+    }
+    for (int64_t i = chunks * 4; i < chunks * 4 + rem; ++i) {
+        const v8 wi = bc8(f32 ? wf[i] : (float)w8[i]);
+        s[0][0] += ld8(hT + i * TB) * wi;
+        s[0][1] += ld8(hT + i * TB + 8) * wi;
+    }
+    v8 r0 = s[0][0] + s[1][0] + s[2][0] + s[3][0], r1 = s[0][1] + s[1][1] + s[2][1] + s[3][1];
+    if (!f32) {
+        r0 *= bc8(w.s[j]);
+        r1 *= bc8(w.s[j]);
+    }
+    st8(res, r0);
+    st8(res + 8, r1);
+}
+
+// out[b][j] = row(j) of token b for b < bs, j < out_f: tokens transposed into blocks of TB,
+// rows spread over the threads.
+template <class Row>
+void rows_over_token_blocks(const float* hb, int64_t bs, int64_t in_f, int64_t out_f, float* out, Row row) {
+    const int64_t nblk = (bs + TB - 1) / TB;
+    std::vector<float> hT((size_t)(nblk * in_f * TB));
+#pragma omp parallel for schedule(static)
+    for (int64_t blk = 0; blk < nblk; ++blk)
+        transpose_tokens(hb, in_f, blk * TB, std::min<int64_t>(TB, bs - blk * TB), &hT[blk * in_f * TB]);
+#pragma omp parallel for schedule(static)
+    for (int64_t j = 0; j < out_f; ++j) {
+        for (int64_t blk = 0; blk < nblk; ++blk) {
+            float res[TB];
+            row(&hT[blk * in_f * TB], j, res);
+            const int64_t nb = std::min<int64_t>(TB, bs - blk * TB);
+            for (int64_t t = 0; t < nb; ++t) out[(blk * TB + t) * out_f + j] = res[t];
+        }
+    }
+}
+
+void gemm_cpu(const float* hb, const WView& w, int64_t bs, int64_t in_f, int64_t out_f, float* out) {
+    if (!g_fast) {
+        gemm_cpu_scalar(hb, w, bs, in_f, out_f, out);
+        return;
+    }
+    if (w.fmt == Q4_ROW)
+        rows_over_token_blocks(hb, bs, in_f, out_f, out,
+                               [&](const float* hT, int64_t j, float* r) { block_row_q4x4(hT, in_f, w, j, r); });
+    else
+        rows_over_token_blocks(hb, bs, in_f, out_f, out,
+                               [&](const float* hT, int64_t j, float* r) { block_row_single(hT, in_f, w, j, r); });
+}
+
+// matvec_mul_into of each of bs tokens (the prefill's per-token MLP GEMVs).
+void matvec_into_tokens(const float* hb, int64_t bs, int64_t in_f, const WView& w, float* out, int64_t out_f) {
+    if (!g_fast) {
+        for (int64_t b = 0; b < bs; ++b) matvec_mul_into(hb + b * in_f, in_f, w, out + b * out_f, out_f);
+        return;
+    }
+    rows_over_token_blocks(hb, bs, in_f, out_f, out,
+                           [&](const float* hT, int64_t j, float* r) { block_row_into(hT, in_f, w, j, r); });
 }
 
 // rms_norm_into / rms_norm_cpu: cpu_engine.rs:1275-1302.
@@ -306,6 +471,94 @@ void attend_row(const float* q, const float* kc, const float* vc, int64_t kv_len
             const float inv = 1.0f / l;
             for (int64_t d = 0; d < hd; ++d) oh[d] = o[d] * inv;
         }
+    }
+}
+
+// attend_row's chains for the query heads [h0, h0 + nh) that share KV head g (nh <= 8,
+// hd <= 128): each head keeps its own online softmax over the rows in order; only the q.k
+// dot products of 8 consecutive rows are formed side by side (one lane per head, each dot
+// summed over d in order), so every output equals attend_row's.
+void attend_group(const float* q, int64_t h0, int64_t nh, int64_t g, const float* kc, const float* vc,
+                  int64_t kv_len, int64_t nkv, int64_t hd, float* out, bool div_out) {
+    const float scale = 1.0f / std::sqrt((float)hd);
+    alignas(32) float qT[128 * 8];
+    for (int64_t d = 0; d < hd; ++d)
+        for (int hh = 0; hh < 8; ++hh) qT[d * 8 + hh] = hh < nh ? q[(h0 + hh) * hd + d] : 0.f;
+    std::vector<float> o((size_t)(nh * hd), 0.f);
+    float m[8], l[8];
+    for (int hh = 0; hh < 8; ++hh) {
+        m[hh] = -INFINITY;
+        l[hh] = 0.f;
+    }
+    for (int64_t t0 = 0; t0 < kv_len; t0 += 8) {
+        const int64_t nr = std::min<int64_t>(8, kv_len - t0);
+        alignas(32) float dots[8][8] = {};
+        const float* kr[8];
+        for (int r = 0; r < 8; ++r) kr[r] = kc + (std::min<int64_t>(t0 + r, kv_len - 1) * nkv + g) * hd;  // padding rows unused
+        for (int64_t d = 0; d < hd; ++d) {
+            const float* qd = qT + d * 8;
+            for (int r = 0; r < 8; ++r) {
+                const float kv = kr[r][d];
+                for (int hh = 0; hh < 8; ++hh) dots[r][hh] += qd[hh] * kv;
+            }
+        }
+        for (int64_t r = 0; r < nr; ++r) {
+            const float* vh = vc + ((t0 + r) * nkv + g) * hd;
+            for (int64_t hh = 0; hh < nh; ++hh) {
+                const float score = dots[r][hh] * scale;
+                float* oh = &o[hh * hd];
+                if (score > m[hh]) {
+                    const float e = expf(m[hh] - score);
+                    l[hh] = l[hh] * e + 1.0f;
+                    for (int64_t d = 0; d < hd; ++d) oh[d] = oh[d] * e + vh[d];
+                    m[hh] = score;
+                } else {
+                    const float e = expf(score - m[hh]);
+                    l[hh] += e;
+                    for (int64_t d = 0; d < hd; ++d) oh[d] += e * vh[d];
+                }
+            }
+        }
+    }
+    for (int64_t hh = 0; hh < nh; ++hh) {
+        float* dst = out + (h0 + hh) * hd;
+        const float* oh = &o[hh * hd];
+        if (div_out) {
+            for (int64_t d = 0; d < hd; ++d) dst[d] = oh[d] / l[hh];
+        } else {
+            const float inv = 1.0f / l[hh];
+            for (int64_t d = 0; d < hd; ++d) dst[d] = oh[d] * inv;
+        }
+    }
+}
+
+// Decode attention of one query row: attend_row, or its chains one head per task.
+void attend_decode(const float* q, const float* kc, const float* vc, int64_t kv_len, int64_t nq, int64_t nkv,
+                   int64_t hd, float* out) {
+    if (!g_fast || hd > 128) {
+        attend_row(q, kc, vc, kv_len, nq, nkv, hd, out, false);
+        return;
+    }
+    const int64_t per = nq / nkv;
+#pragma omp parallel for schedule(static)
+    for (int64_t h = 0; h < nq; ++h) attend_group(q, h, 1, h / per, kc, vc, kv_len, nkv, hd, out, false);
+}
+
+// Prefill attention of bs query rows at positions start_pos + b, each over cache rows
+// [0, start_pos + b] (flash_attention_cpu): attend_row per row, or its chains as tasks of one
+// row and one KV head's query heads.
+void attend_prefill(const float* qb, const float* kc, const float* vc, int64_t bs, int64_t start_pos, int64_t nq,
+                    int64_t nkv, int64_t hd, float* out) {
+    const int64_t per = nq / nkv;
+    if (!g_fast || hd > 128 || per > 8) {
+        for (int64_t b = 0; b < bs; ++b)
+            attend_row(qb + b * nq * hd, kc, vc, start_pos + b + 1, nq, nkv, hd, out + b * nq * hd, true);
+        return;
+    }
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t task = 0; task < bs * nkv; ++task) {
+        const int64_t b = task / nkv, g = task % nkv;
+        attend_group(qb + b * nq * hd, g * per, per, g, kc, vc, start_pos + b + 1, nkv, hd, out + b * nq * hd, true);
     }
 }
 
@@ -423,6 +676,7 @@ int orc_quantize_q4g32(const float* w, int64_t n, int64_t k, uint8_t* q, uint16_
 // w = (nib - 8) * f32(scale16): exact in f32 (a 4-bit integer times an 11-bit mantissa).
 void orc_dequantize_q4g32(const uint8_t* q, const uint16_t* s16, int64_t n, int64_t k, float* w) {
     const int64_t G = k / 32;
+#pragma omp parallel for schedule(static) if (n * k > (1 << 20))
     for (int64_t j = 0; j < n; ++j)
         for (int64_t i = 0; i < k / 2; ++i) {
             const uint8_t b = q[j * (k / 2) + i];
@@ -464,15 +718,16 @@ void orc_rope_thetas(int64_t hd, float theta, float* out) { rope_thetas(hd, thet
 void orc_apply_rope(float* v, int64_t pos, int64_t nh, int64_t hd, float theta) { apply_rope(v, pos, nh, hd, theta); }
 void orc_attn_decode(const float* q, const float* kc, const float* vc, int64_t kv_len, int64_t nq, int64_t nkv,
                      int64_t hd, float* out) {
-    attend_row(q, kc, vc, kv_len, nq, nkv, hd, out, false);
+    attend_decode(q, kc, vc, kv_len, nq, nkv, hd, out);
 }
 // flash_attention_cpu: block of `bs` query rows at absolute positions start_pos+b,
 // each attending to cache rows [0, start_pos+b] (cpu_engine.rs:1151-1214).
 void orc_attn_prefill(const float* qb, const float* kc, const float* vc, int64_t bs, int64_t start_pos, int64_t nq,
                       int64_t nkv, int64_t hd, float* out) {
-    for (int64_t b = 0; b < bs; ++b)
-        attend_row(qb + b * nq * hd, kc, vc, start_pos + b + 1, nq, nkv, hd, out + b * nq * hd, true);
+    attend_prefill(qb, kc, vc, bs, start_pos, nq, nkv, hd, out);
 }
+// 1: token-blocked / parallel forms (default); 0: the scalar loops they are pinned against.
+void orc_set_fast(int on) { g_fast = on ? 1 : 0; }
 void orc_silu_mul(const float* g, const float* u, int64_t n, float* out) {
     for (int64_t i = 0; i < n; ++i) out[i] = silu_mul(g[i], u[i]);
 }
@@ -699,8 +954,15 @@ int64_t orc_sample_topk(const float* penalized, int64_t V, float temperature, in
 // argmax, stop after emitting 2 / 151645 / 151643.
 // raw_logits (optional, max_new * V floats) receives each step's logits BEFORE the
 // penalty. Returns the number of generated ids written to out_ids.
-int64_t orc_generate(void* p, const uint32_t* prompt, int64_t n_prompt, int64_t max_new, uint32_t* out_ids,
-                     float* raw_logits) {
+//
+// With a prefix-cache hit (cpu_engine.rs:2518-2534, 2577-2582) the caches start as the
+// entry's rows: k_in / v_in [n_layers][prefix_len][n_kv * head_dim], and the prefill runs
+// from position prefix_len (:2590-2606). k_out / v_out (optional) receive the caches after
+// the prefill, the rows save_prefix stores (:2746-2756): [n_layers][rows][n_kv * head_dim]
+// with rows = the prefill end (at most max_context with eviction), written to *kv_rows_out.
+int64_t orc_generate_ex(void* p, const uint32_t* prompt, int64_t n_prompt, int64_t max_new, uint32_t* out_ids,
+                        float* raw_logits, int64_t prefix_len, const float* k_in, const float* v_in, float* k_out,
+                        float* v_out, int64_t* kv_rows_out) {
     OrcModel* m = (OrcModel*)p;
     const orc_config& c = m->c;
     const int64_t H = c.hidden, NQ = c.n_heads, NKV = c.n_kv_heads, HD = c.head_dim, QD = NQ * HD, KD = NKV * HD,
@@ -709,14 +971,25 @@ int64_t orc_generate(void* p, const uint32_t* prompt, int64_t n_prompt, int64_t 
     std::vector<uint32_t> tokens(prompt, prompt + n_prompt);
     if (tokens.empty()) tokens.push_back(1);  // :2487-2489
     std::vector<KvCache> kv(NL);
+    if (k_in && v_in && prefix_len > 0)
+        for (int64_t l = 0; l < NL; ++l) {
+            kv[l].k.assign(k_in + l * prefix_len * KD, k_in + (l + 1) * prefix_len * KD);
+            kv[l].v.assign(v_in + l * prefix_len * KD, v_in + (l + 1) * prefix_len * KD);
+        }
+    else
+        prefix_len = 0;
     const WView lm{F32, m->lm.empty() ? m->embed.data() : m->lm.data(), nullptr, nullptr, nullptr};
 
     // ---- prefill ----
     const int64_t pre_end = tokens.size() > 1 ? (int64_t)tokens.size() - 1 : 0;
-    std::vector<float> g(I), u(I), mm(I), mlp_out(H);
-    for (int64_t pos = 0; pos < pre_end; pos += 64) {
+    // flash_attention_cpu reads rows [0, pos] of the cache by absolute position (:1166-1170):
+    // once eviction has dropped rows that is past the cache's end, where the reference's slice
+    // indexing panics. The oracle refuses the same inputs.
+    if (c.max_context > 0 && pre_end > c.max_context) return -1;
+    for (int64_t pos = prefix_len; pos < pre_end; pos += 64) {
         const int64_t end = std::min(pos + 64, pre_end), bs = end - pos;
-        std::vector<float> x(bs * H), hb(bs * H), qb(bs * QD), kb(bs * KD), vb(bs * KD), ctx(bs * QD), ob(bs * H);
+        std::vector<float> x(bs * H), hb(bs * H), qb(bs * QD), kb(bs * KD), vb(bs * KD), ctx(bs * QD), ob(bs * H),
+            h2(bs * H), g(bs * I), u(bs * I), mm(bs * I), dn(bs * H);
         for (int64_t i = 0; i < bs; ++i) {
             const int64_t id = tokens[pos + i] % V;
             std::memcpy(&x[i * H], &m->embed[id * H], H * 4);
@@ -742,14 +1015,14 @@ int64_t orc_generate(void* p, const uint32_t* prompt, int64_t n_prompt, int64_t 
             for (int64_t i = 0; i < bs; ++i) {
                 if (!L.bv.empty()) for (int64_t j = 0; j < KD; ++j) vb[i * KD + j] += L.bv[j];
             }
+#pragma omp parallel for schedule(static) if (g_fast)
             for (int64_t i = 0; i < bs; ++i) {
                 apply_rope(&qb[i * QD], pos + i, NQ, HD, theta);
                 apply_rope(&kb[i * KD], pos + i, NKV, HD, theta);
             }
             kv_append(kv[l], kb.data(), vb.data(), bs, KD, c.max_context, c.sink_tokens);
             // flash_attention_cpu indexes the cache by absolute position (:2700-2704)
-            for (int64_t b = 0; b < bs; ++b)
-                attend_row(&qb[b * QD], kv[l].k.data(), kv[l].v.data(), pos + b + 1, NQ, NKV, HD, &ctx[b * QD], true);
+            attend_prefill(qb.data(), kv[l].k.data(), kv[l].v.data(), bs, pos, NQ, NKV, HD, ctx.data());
             if (bs == 1) {
                 matvec_mul(ctx.data(), QD, L.o.view(), ob.data(), H);
             } else {
@@ -758,20 +1031,34 @@ int64_t orc_generate(void* p, const uint32_t* prompt, int64_t n_prompt, int64_t 
             if (!L.bo.empty())
                 for (int64_t i = 0; i < bs; ++i)
                     for (int64_t j = 0; j < H; ++j) ob[i * H + j] += L.bo[j];
+            // per token: residual, norm, run_mlp_into (:2718-2742); the MLP GEMVs of the chunk's
+            // tokens run as one token-blocked pass of matvec_mul_into
             for (int64_t i = 0; i < bs; ++i) {
                 float* xr = &x[i * H];
                 for (int64_t d = 0; d < H; ++d) xr[d] += ob[i * H + d];
-                std::vector<float> h2(H);
-                rms_norm(xr, L.ln2.data(), eps, h2.data(), H);
-                mlp(h2.data(), L.gate.view(), L.up.view(), L.down.view(), H, I, g.data(), u.data(), mm.data(),
-                    mlp_out.data());
-                for (int64_t d = 0; d < H; ++d) xr[d] += mlp_out[d];
+                rms_norm(xr, L.ln2.data(), eps, &h2[i * H], H);
             }
+            matvec_into_tokens(h2.data(), bs, H, L.gate.view(), g.data(), I);
+            matvec_into_tokens(h2.data(), bs, H, L.up.view(), u.data(), I);
+            for (int64_t e = 0; e < bs * I; ++e) {
+                const float sg = g[e] * (1.0f / (1.0f + expf(-g[e])));
+                mm[e] = sg * u[e];
+            }
+            matvec_into_tokens(mm.data(), bs, I, L.down.view(), dn.data(), H);
+            for (int64_t i = 0; i < bs; ++i)
+                for (int64_t d = 0; d < H; ++d) x[i * H + d] += dn[i * H + d];
         }
     }
+    if (kv_rows_out) *kv_rows_out = (int64_t)kv[0].k.size() / KD;
+    if (k_out && v_out)
+        for (int64_t l = 0; l < NL; ++l) {
+            std::memcpy(k_out + l * (int64_t)kv[l].k.size(), kv[l].k.data(), kv[l].k.size() * 4);
+            std::memcpy(v_out + l * (int64_t)kv[l].v.size(), kv[l].v.data(), kv[l].v.size() * 4);
+        }
 
     // ---- decode ----
     std::vector<float> x(H), h(H), q(QD), k(KD), v(KD), att(QD), o(H), h2(H), down(H), fn(H), logits(V);
+    std::vector<float> g(I), u(I), mm(I);
     std::vector<uint32_t> gen;
     while ((int64_t)gen.size() < max_new) {
         const int64_t id = tokens.back() % V;
@@ -790,7 +1077,7 @@ int64_t orc_generate(void* p, const uint32_t* prompt, int64_t n_prompt, int64_t 
             apply_rope(k.data(), pos, NKV, HD, theta);
             kv_append(kv[l], k.data(), v.data(), 1, KD, c.max_context, c.sink_tokens);
             const int64_t kv_len = (int64_t)kv[l].k.size() / KD;
-            attend_row(q.data(), kv[l].k.data(), kv[l].v.data(), kv_len, NQ, NKV, HD, att.data(), false);
+            attend_decode(q.data(), kv[l].k.data(), kv[l].v.data(), kv_len, NQ, NKV, HD, att.data());
             matvec_mul_into(att.data(), QD, L.o.view(), o.data(), H);
             if (!L.bo.empty()) for (int64_t j = 0; j < H; ++j) o[j] += L.bo[j];
             for (int64_t d = 0; d < H; ++d) x[d] += o[d];
@@ -811,6 +1098,14 @@ int64_t orc_generate(void* p, const uint32_t* prompt, int64_t n_prompt, int64_t 
     return (int64_t)gen.size();
 }
 
+int64_t orc_generate(void* p, const uint32_t* prompt, int64_t n_prompt, int64_t max_new, uint32_t* out_ids,
+                     float* raw_logits) {
+    return orc_generate_ex(p, prompt, n_prompt, max_new, out_ids, raw_logits, 0, nullptr, nullptr, nullptr, nullptr,
+                           nullptr);
+}
+
 int orc_num_threads(void) { return omp_get_max_threads(); }
+// Thread count of the following calls (tests check that results do not depend on it).
+void orc_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
 
 }  // extern "C"

@@ -231,3 +231,44 @@ def test_attention_ragged_and_short(plane):
     _attn_case(plane, [130, 7, 64], nq=28, nkv=4, hd=128, seed=6, align=64)
     _attn_case(plane, [5, 300], kv_f16=False, seed=2)
     _attn_case(plane, [130, 7], nq=28, nkv=4, hd=128, seed=3)  # Qwen2-7B heads
+
+
+def _attn_inputs(plane, B, T, seed, nq=14, nkv=2, hd=64):
+    """Device inputs of a batch of B sequences of T rows (fp16 tile layout, 64-row regions)."""
+    D = lambda a: ops.DeviceArray.from_numpy(plane, a)  # noqa: E731
+    rng = np.random.default_rng(seed)
+    k = rng.standard_normal((nkv, B * T, hd)).astype(np.float16)
+    v = rng.standard_normal((nkv, B * T, hd)).astype(np.float16)
+    kp, vp = ops.pack_kv_f16(k, v)
+    q = rng.standard_normal((B, nq * hd)).astype(np.float32)
+    offs = (np.arange(B) * T).astype(np.int64)
+    return [D(q), D(kp), D(vp), D(offs), D(np.full(B, T, np.int32))]
+
+
+def test_attention_on_two_streams_keeps_split_scratch_apart(plane):
+    """Split attention calls queued on two caller streams at once (no synchronisation between
+    them) each use their own stream's partials and merge counters: every output equals the same
+    call made alone on the context's stream."""
+    import ctypes
+
+    from bramha_amd._lib import check, lib
+
+    hip = ctypes.CDLL("libamdhip64.so.7")  # the runtime the library already loaded (same soname)
+    streams = [ctypes.c_void_p(), ctypes.c_void_p()]
+    for s in streams:
+        assert hip.hipStreamCreate(ctypes.byref(s)) == 0
+    nq, nkv, hd, T, B = 14, 2, 64, 4096, 8
+    ins = [_attn_inputs(plane, B, T, seed=70 + i) for i in range(2)]
+    want = [ops.attn_decode(plane, *x, nq, nkv, hd, T).numpy() for x in ins]
+    outs = [[ops.DeviceArray(plane, (B, nq * hd), np.float32) for _ in range(6)] for _ in range(2)]
+    for r in range(6):
+        for i in range(2):
+            q, k, v, off, ln = ins[i]
+            check(lib.bh_attn_decode(plane.ctx, q.ptr, k.ptr, v.ptr, 1, B * T, off.ptr, ln.ptr, B, nq, nkv, hd, T,
+                                     outs[i][r].ptr, streams[i]), plane.ctx)
+    ops.synchronize(plane)
+    for i in range(2):
+        for r in range(6):
+            assert np.array_equal(outs[i][r].numpy(), want[i]), (i, r)
+    for s in streams:
+        assert hip.hipStreamDestroy(s) == 0
