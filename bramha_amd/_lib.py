@@ -91,6 +91,8 @@ _PROTOS = {
     "bh_rope": (c_int, [_P, _P, _P, c_int, c_int, c_int, c_float, c_int, _P]),
     "bh_silu_mul": (c_int, [_P, _P, _P, _P, c_int64, _P]),
     "bh_attn_decode": (c_int, [_P, _P, _P, _P, c_int, c_int64, _P, _P, c_int, c_int, c_int, c_int, c_int, _P, _P]),
+    "bh_attn_decode_noalloc": (c_int, [_P, _P, _P, _P, c_int, c_int64, _P, _P, c_int, c_int, c_int, c_int, c_int, _P,
+                                       _P]),
     "bh_time_gemv": (c_int, [_P, _P, _P, _P, c_int, c_int, c_size_t, POINTER(c_double)]),
     "bh_time_attn": (c_int, [_P, _P, _P, _P, c_int, c_int64, _P, _P, c_int, c_int, c_int, c_int, c_int, _P, c_int,
                              c_size_t, POINTER(c_double)]),

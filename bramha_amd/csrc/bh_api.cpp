@@ -280,6 +280,37 @@ static int matvec_common(bh_ctx* ctx, int fmt, const float* h, size_t in_f, cons
     return BH_OK;
 }
 
+// ------------------------------------------------ no-allocation attention scratch
+// Scratch of bh_attn_decode_noalloc: NOALLOC_PART_BYTES of split partials, then NOALLOC_COUNTERS
+// int32 split-merge counters. Every launch leaves the counters at zero (the last workgroup of
+// each (row, KV head) resets its own); they are cleared once per device at bh_init. Each device
+// holds its own copy until the process ends. In host code the name `scratch` stands for the
+// array but is not its device address: that is resolved per device with hipGetSymbolAddress and
+// only that address is used.
+constexpr size_t NOALLOC_PART_BYTES = (size_t)2 << 20;
+constexpr int NOALLOC_COUNTERS = 4096;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_PART_BYTES + (size_t)NOALLOC_COUNTERS * 4];
+
+static std::mutex g_noalloc_mu;
+static uint8_t* g_noalloc_ptr[256] = {};  // per device ordinal
+
+// Resolve this device's copy of `scratch` (the device is current) and clear its counters once.
+static int noalloc_setup(bh_ctx* c) {
+    if (c->device < 0 || c->device >= 256) return c->fail(BH_ERR_UNSUPPORTED, "device ordinal above 255");
+    std::lock_guard<std::mutex> g(g_noalloc_mu);
+    if (!g_noalloc_ptr[c->device]) {
+        uint8_t* p = nullptr;
+        hipError_t e = hipGetSymbolAddress((void**)&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return c->hip_fail(e, "hipGetSymbolAddress(no-allocation scratch)");
+        e = hipMemsetAsync(p + NOALLOC_PART_BYTES, 0, (size_t)NOALLOC_COUNTERS * 4, c->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) return c->hip_fail(e, "clearing the no-allocation scratch");
+        g_noalloc_ptr[c->device] = p;
+    }
+    c->noalloc_scratch = g_noalloc_ptr[c->device];
+    return BH_OK;
+}
+
 extern "C" {
 
 const char* bh_status_str(int s) {
@@ -322,6 +353,13 @@ int bh_init(int device, bh_ctx** out) {
         hipStreamDestroy(c->stream);
         delete c;
         return BH_ERR_OOM;
+    }
+    if (noalloc_setup(c) != BH_OK) {
+        hipFree(c->split_part);
+        hipFree(c->split_cnt);
+        hipStreamDestroy(c->stream);
+        delete c;
+        return BH_ERR_HIP;
     }
     *out = c;
     return BH_OK;
@@ -634,6 +672,32 @@ int bh_attn_decode(bh_ctx* ctx, const float* q, const void* k, const void* v, in
     rc = attn_args(ctx, st, q, k, v, kv_f16, kv_rows, seq_off, seq_len, batch, n_q, n_kv, head_dim, max_len, out, a);
     if (rc) return rc;
     hipError_t e = launch_attention(a, st);
+    return e == hipSuccess ? BH_OK : ctx->hip_fail(e, "attention launch");
+}
+
+int bh_attn_decode_noalloc(bh_ctx* ctx, const float* q, const void* k, const void* v, int kv_f16, int64_t kv_rows,
+                           const int64_t* seq_off, const int32_t* seq_len, int batch, int n_q, int n_kv,
+                           int head_dim, int max_len, float* out, void* stream) {
+    int rc = attn_check(ctx, q, k, v, kv_f16, kv_rows, seq_off, seq_len, out, batch, n_q, n_kv, head_dim, max_len);
+    if (rc) return rc;
+    if (batch == 0) return BH_OK;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    if (!ctx->noalloc_scratch) return ctx->fail(BH_ERR_HIP, "no-allocation scratch not set up");
+    AttnArgs a;
+    attn_fill(q, k, v, kv_f16, kv_rows, seq_off, seq_len, batch, n_q, n_kv, head_dim, max_len, out, a);
+    if (a.splits > 1) {
+        const size_t need = (size_t)batch * n_q * a.splits * (head_dim + 2) * 4;
+        if (need > NOALLOC_PART_BYTES || (int64_t)batch * n_kv > NOALLOC_COUNTERS)
+            return ctx->fail(BH_ERR_CAPACITY, "attention split scratch of " + std::to_string(need) + " bytes and " +
+                                                  std::to_string((int64_t)batch * n_kv) +
+                                                  " counters exceeds the no-allocation scratch (" +
+                                                  std::to_string(NOALLOC_PART_BYTES) + " bytes, " +
+                                                  std::to_string(NOALLOC_COUNTERS) + " counters)");
+        a.part_o = (float*)ctx->noalloc_scratch;
+        a.part_ml = a.part_o + (size_t)batch * n_q * a.splits * head_dim;
+        a.cnt = (int32_t*)(ctx->noalloc_scratch + NOALLOC_PART_BYTES);
+    }
+    hipError_t e = launch_attention(a, pick(ctx, stream));
     return e == hipSuccess ? BH_OK : ctx->hip_fail(e, "attention launch");
 }
 

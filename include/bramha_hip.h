@@ -152,6 +152,18 @@ int bh_attn_decode(bh_ctx* ctx, const float* q, const void* k, const void* v, in
                    const int64_t* seq_off, const int32_t* seq_len, int batch, int n_q, int n_kv, int head_dim,
                    int max_len, float* out, void* stream);
 
+/* bh_attn_decode without any device allocation (no counterpart in the reference: for callers that
+ * cannot allocate, e.g. code under HIP graph capture or a serving loop that forbids hipMalloc).
+ * Same arguments, kernels and results as bh_attn_decode; the split partials and merge counters live
+ * in a fixed scratch array of 2 MiB + 4096 counters that each device holds for the life of the
+ * process, shared by every call on that device. A call whose split plan needs more
+ * (batch * n_q * splits * (head_dim + 2) * 4 bytes of partials, batch * n_kv counters) fails with
+ * BH_ERR_CAPACITY. Calls that overlap on one device (other streams, other contexts) race on the
+ * shared scratch: the caller orders them. */
+int bh_attn_decode_noalloc(bh_ctx* ctx, const float* q, const void* k, const void* v, int kv_f16, int64_t kv_rows,
+                           const int64_t* seq_off, const int32_t* seq_len, int batch, int n_q, int n_kv,
+                           int head_dim, int max_len, float* out, void* stream);
+
 /* ------------------------------------------------------------ measurement */
 /* Measurement helpers (no counterpart in the reference; used by bench.py for the GEMV and
  * attention sweeps). Each replays a HIP graph of `iters` launches on the context's stream whose
