@@ -96,6 +96,7 @@ _PROTOS = {
     "bh_time_gemv": (c_int, [_P, _P, _P, _P, c_int, c_int, c_size_t, POINTER(c_double)]),
     "bh_time_attn": (c_int, [_P, _P, _P, _P, c_int, c_int64, _P, _P, c_int, c_int, c_int, c_int, c_int, _P, c_int,
                              c_size_t, POINTER(c_double)]),
+    "bh_time_probe": (c_int, [_P, c_int, c_size_t, c_int, c_int, c_int, POINTER(c_double)]),
     "bh_model_create": (c_int, [_P, POINTER(bh_model_config), POINTER(c_void_p)]),
     "bh_model_load_dir": (c_int, [_P, c_char_p, POINTER(c_int)]),
     "bh_model_kv_read": (c_int, [_P, c_int, c_int64, c_int64, _P, _P]),

@@ -20,6 +20,7 @@ SOURCES = [
     "csrc/k_attn.hip",
     "csrc/k_attn_o.hip",
     "csrc/k_ops.hip",
+    "csrc/k_probe.hip",
     "csrc/bh_host.cpp",
     "csrc/bh_api.cpp",
     "csrc/bh_model.cpp",

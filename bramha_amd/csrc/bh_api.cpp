@@ -786,6 +786,28 @@ int bh_time_gemv(bh_ctx* ctx, const bh_weight* wh, const float* x, float* y, int
     return rc;
 }
 
+int bh_time_probe(bh_ctx* ctx, int copy, size_t bytes, int wgs, int unroll, int iters, double* us_per_launch) {
+    if (!ctx || bytes < 16 || wgs <= 0 || wgs > (1 << 20) || iters <= 0 || !us_per_launch ||
+        !(unroll == 4 || unroll == 8 || unroll == 16))
+        return BH_ERR_INVALID;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    bytes &= ~(size_t)15;
+    void *src = nullptr, *dst = nullptr, *sink = nullptr;
+    hipError_t e = hipMalloc(&src, bytes);
+    if (e == hipSuccess) e = hipMemset(src, 0x5a, bytes);
+    if (e == hipSuccess && copy) e = hipMalloc(&dst, bytes);
+    if (e == hipSuccess && !copy) e = hipMalloc(&sink, (size_t)wgs * 256 * 4);
+    int rc = e == hipSuccess ? BH_OK : ctx->hip_fail(e, "hipMalloc(probe buffers)");
+    if (rc == BH_OK)
+        rc = time_graph(ctx, iters, [&](int, hipStream_t st) {
+            return launch_probe(copy, src, dst, (int64_t)bytes, wgs, unroll, (uint32_t*)sink, st);
+        }, us_per_launch);
+    if (src) hipFree(src);
+    if (dst) hipFree(dst);
+    if (sink) hipFree(sink);
+    return rc;
+}
+
 int bh_time_attn(bh_ctx* ctx, const float* q, const void* k, const void* v, int kv_f16, int64_t kv_rows,
                  const int64_t* seq_off, const int32_t* seq_len, int batch, int n_q, int n_kv, int head_dim,
                  int max_len, float* out, int iters, size_t rotate_bytes, double* us_per_launch) {

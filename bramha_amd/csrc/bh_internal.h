@@ -278,6 +278,12 @@ void attn_plan(int max_len, int batch, int nkv, int hd, int* splits, int* split_
 bool attn_o_fusable(int fmt, const AttnArgs& at, const GemvArgs& o);
 hipError_t launch_attn_o(int fmt, const AttnArgs& at, const GemvArgs& o, hipStream_t st);
 
+// k_probe.hip — HBM bandwidth probes: copy = 0 streams `bytes` of src with 16-byte non-temporal
+// loads (sink: wgs * 256 words, written only on an impossible value), copy = 1 copies src to dst;
+// wgs workgroups of 256 threads, `unroll` (4, 8, 16) loads in flight per thread.
+hipError_t launch_probe(int copy, const void* src, void* dst, int64_t bytes, int wgs, int unroll, uint32_t* sink,
+                        hipStream_t st);
+
 // ---------------------------------------------------------------------------
 // Host helpers (bh_host.cpp)
 // ---------------------------------------------------------------------------

@@ -93,9 +93,12 @@ struct bh_model {
 
     int B = 0;
     std::vector<int32_t> bslots;
+    std::vector<char> stale;       // entry's slot was reopened: it must be replaced before a decode
     hipGraph_t graph = nullptr;
     hipGraphExec_t gexec = nullptr;
     int g_B = 0, g_splits = 0, g_rows = 0;
+    std::vector<int64_t> g_off;    // region offsets the captured step holds as launch arguments
+    int64_t g_cap = 0;             // and the smallest region capacity it assumes
 
     bool timing = false;
     std::vector<TimerRec> recs;
@@ -368,6 +371,8 @@ void drop_graph(bh_model* m) {
     m->gexec = nullptr;
     m->graph = nullptr;
     m->g_B = m->g_splits = m->g_rows = 0;
+    m->g_off.clear();
+    m->g_cap = 0;
 }
 
 // Largest attention length the next n_steps decode steps of the batch can reach.
@@ -386,6 +391,9 @@ int check_decode_room(bh_model* m, int n_steps) {
     for (int b = 0; b < m->B; ++b) {
         const int s = m->bslots[b];
         if (!m->open_h[s]) return m->fail(BH_ERR_INVALID, "decode batch holds a slot that is not open");
+        if (m->stale[b])
+            return m->fail(BH_ERR_INVALID, "the slot of batch entry " + std::to_string(b) +
+                                               " was reopened: replace the entry (bh_model_decode_replace) first");
         const int64_t end = m->len_h[s] + n_steps;
         if (end > m->max_pos) return m->fail(BH_ERR_CAPACITY, "position beyond the RoPE table");
         if (m->c.max_context <= 0 && end > m->cap_h[s])
@@ -649,8 +657,11 @@ int bh_model_seq_open(bh_model* m, int slot, int64_t capacity) {
     if (m->c.max_context > 0) capacity = m->c.max_context;
     if (capacity <= 0) return m->fail(BH_ERR_INVALID, "capacity must be positive");
     capacity = (capacity + m->kv_align - 1) / m->kv_align * m->kv_align;  // keeps regions aligned
+    // a slot of the decode batch may be reopened for a new sequence (it keeps its region when the
+    // capacity fits); its batch entry must then be replaced before the next decode
+    int in_batch = -1;
     for (int b = 0; b < m->B; ++b)
-        if (m->bslots[b] == slot) return m->fail(BH_ERR_INVALID, "slot is in the decode batch; replace it first");
+        if (m->bslots[b] == slot) in_batch = b;
     if (m->off_h[slot] < 0 || m->cap_h[slot] < capacity) {
         if (m->next_free + capacity > m->c.kv_rows)
             return m->fail(BH_ERR_CAPACITY, "packed KV buffer full: " + std::to_string(m->next_free) + " + " +
@@ -661,6 +672,7 @@ int bh_model_seq_open(bh_model* m, int slot, int64_t capacity) {
     }
     m->len_h[slot] = 0;
     m->open_h[slot] = 1;
+    if (in_batch >= 0) m->stale[in_batch] = 1;
     // repetition-penalty counts of the slot start at zero (an eager copy-engine fill, never captured)
     hipError_t e = hipMemsetAsync(m->d_pen + (size_t)slot * m->c.vocab, 0, (size_t)m->c.vocab * 2, m->st);
     if (e == hipSuccess) e = hipStreamSynchronize(m->st);
@@ -795,6 +807,7 @@ int bh_model_decode_setup(bh_model* m, int batch, const int32_t* slots, const ui
     drop_graph(m);  // the captured step holds the entries' KV offsets as launch arguments
     m->B = batch;
     m->bslots.assign(slots, slots + batch);
+    m->stale.assign(batch, 0);
     for (int b = 0; b < batch; ++b) {
         hipError_t e = set_entry(m, b, slots[b], first_tokens[b]);
         if (e != hipSuccess) return m->ctx->hip_fail(e, "decode_setup");
@@ -810,7 +823,11 @@ int bh_model_decode_replace(bh_model* m, int b, int slot, uint32_t first_token) 
     for (int i = 0; i < m->B; ++i)
         if (i != b && m->bslots[i] == slot) return m->fail(BH_ERR_INVALID, "slot already in the batch");
     m->bslots[b] = slot;
-    drop_graph(m);  // the captured step holds the entries' KV offsets as launch arguments
+    m->stale[b] = 0;
+    // the captured step holds the entries' region offsets and the smallest capacity as launch
+    // arguments: it stays valid when the new sequence has the old region (a reopened slot)
+    if (m->gexec && ((int)m->g_off.size() <= b || m->g_off[b] != m->off_h[slot] || m->cap_h[slot] < m->g_cap))
+        drop_graph(m);
     hipError_t e = set_entry(m, b, slot, first_token);
     return e == hipSuccess ? BH_OK : m->ctx->hip_fail(e, "decode_replace");
 }
@@ -840,6 +857,12 @@ static int decode_locked(bh_model* m, int n_steps, uint32_t* ids_out, float* raw
         m->g_B = m->B;
         m->g_splits = splits;
         m->g_rows = rows;
+        m->g_off.resize(m->B);
+        m->g_cap = INT64_MAX;
+        for (int b = 0; b < m->B; ++b) {
+            m->g_off[b] = m->off_h[m->bslots[b]];
+            m->g_cap = std::min<int64_t>(m->g_cap, m->cap_h[m->bslots[b]]);
+        }
     }
     int done = 0;
     while (done < n_steps && e == hipSuccess) {

@@ -41,7 +41,9 @@ __global__ void __launch_bounds__(64 * KW * RW) k_gemm_mf(const GemvArgs a0) {
     constexpr int ROWS = 64 * RW;
     constexpr int TB = B / 16;
     constexpr int TOT = NACC * B * ROWS;
-    GemvArgs a = gemv_tokens(a0, (int)blockIdx.y * B, B);
+    // a pass's last group may hold fewer than B valid tokens (a.batch): their activations read as
+    // zero through the buffer resource and the epilogues store only tokens below a.batch
+    GemvArgs a = gemv_tokens(a0, (int)blockIdx.y * B, max(1, min(B, a0.batch - (int)blockIdx.y * B)));
     if (a0.part) a.part = a0.part + (int64_t)blockIdx.y * gridDim.x * TOT;
     if (a0.tile_cnt) a.tile_cnt = a0.tile_cnt + blockIdx.y * (gridDim.x / a0.ksw);
     // S: chunks per pipeline stage (two stages in flight)
@@ -274,7 +276,8 @@ hipError_t launch_e(int epi, const GemvArgs& a, int B, int groups, int rw, hipSt
 }  // namespace
 
 hipError_t launch_gemm_mf(int fmt, int epi, const GemvArgs& a, int B, int rw, hipStream_t st) {
-    if ((B != 16 && B != 32) || a.batch != B || a.ksw < 1 || a.n_pad % 64 || rw < 1 || rw > 2) return hipErrorInvalidValue;
+    if ((B != 16 && B != 32) || a.batch < 1 || a.batch > B || a.ksw < 1 || a.n_pad % 64 || rw < 1 || rw > 2)
+        return hipErrorInvalidValue;
     // A 32-token pass whose launch leaves most CUs idle runs as two 16-token groups: twice the
     // workgroups with no reduction between them (a 16-token pass of 896 x 896 takes 7.7 us, a
     // 32-token one 10.2). Not for the LM head, whose row tiles fill the chip and whose weights
@@ -282,7 +285,7 @@ hipError_t launch_gemm_mf(int fmt, int epi, const GemvArgs& a, int B, int rw, hi
     int groups = 1;
     const int tiles = (a.n_pad + 64 * rw - 1) / (64 * rw);
     const int tot16 = (epi == EPI_SILU ? 2 : 1) * 16 * 64 * rw;
-    if (B == 32 && epi != EPI_LMHEAD && 2 * tiles * a.ksw <= 512 &&
+    if (B == 32 && a.batch > 16 && epi != EPI_LMHEAD && 2 * tiles * a.ksw <= 512 &&
         (a.ksw == 1 || (2 * tiles <= SPLIT_WG_MAX && (int64_t)2 * tiles * a.ksw * tot16 <= (int64_t)SPLIT_WG_MAX * SPLIT_TOT_MAX))) {
         groups = 2;
         B = 16;

@@ -219,9 +219,12 @@ hipError_t launch_gemv(int fmt, int epi, const GemvArgs& a0, hipStream_t st) {
             a.ksw = 1;
             return launch_gemm_pf(fmt, epi, a, st);
         }
-        const bool mf = q4 && rem >= 16;
-        const int B = mf ? (rem >= 32 ? 32 : 16) : (rem >= 8 ? 8 : (rem >= 4 ? 4 : (rem >= 2 ? 2 : 1)));
-        GemvArgs a = gemv_tokens(a0, b0, B);
+        // MFMA passes of 16 or 32 token columns; the last pass of more than 8 tokens takes the
+        // next column count up with only its tokens valid (activations past them read as zero,
+        // nothing of theirs is stored), so a pass of 9..31 tokens is one launch
+        const bool mf = q4 && rem > 8;
+        const int B = mf ? (rem > 16 ? 32 : 16) : (rem >= 8 ? 8 : (rem >= 4 ? 4 : (rem >= 2 ? 2 : 1)));
+        GemvArgs a = gemv_tokens(a0, b0, mf ? std::min(B, rem) : B);
         hipError_t e;
         if (mf) {
             a.ksw = auto_splits(a0, true, 64 * rw, nacc * B * 64 * rw);

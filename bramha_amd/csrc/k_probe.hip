@@ -1,0 +1,79 @@
+// k_probe.hip — HBM bandwidth probes (measurement only; no counterpart in the reference).
+//
+// The read probe streams a buffer larger than the 256 MB Infinity Cache with 16-byte
+// non-temporal loads, U independent loads in flight per thread per round, grid-stride over the
+// buffer, and folds what it read into one word per lane that is stored only if it equals a value
+// the data cannot produce (so the loads stay but nothing is written). The copy probe moves the
+// buffer into a second one with 16-byte non-temporal loads and stores. Together they give the
+// achievable read and copy bandwidth that the GEMV and attention kernels are compared with.
+#include "bh_internal.h"
+
+namespace bh {
+namespace {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <int U>
+__global__ void __launch_bounds__(256) k_read_probe(const u32x4* __restrict__ src, int64_t n16, uint32_t* sink) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    uint32_t acc = 0;
+    for (int64_t i0 = (int64_t)blockIdx.x * 256 + threadIdx.x; i0 < n16; i0 += stride * U) {
+        u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t i = i0 + u * stride;
+            v[u] = i < n16 ? __builtin_nontemporal_load(src + i) : u32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    if (acc == 0x9E3779B9u) sink[(int64_t)blockIdx.x * 256 + threadIdx.x] = acc;
+}
+
+template <int U>
+__global__ void __launch_bounds__(256) k_copy_probe(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
+                                                    int64_t n16) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t i0 = (int64_t)blockIdx.x * 256 + threadIdx.x; i0 < n16; i0 += stride * U) {
+        u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t i = i0 + u * stride;
+            v[u] = i < n16 ? __builtin_nontemporal_load(src + i) : u32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t i = i0 + u * stride;
+            if (i < n16) __builtin_nontemporal_store(v[u], dst + i);
+        }
+    }
+}
+
+}  // namespace
+
+// One probe launch: copy = 0 reads src (sink holds wgs * 256 words), copy = 1 copies src to dst.
+hipError_t launch_probe(int copy, const void* src, void* dst, int64_t bytes, int wgs, int unroll, uint32_t* sink,
+                        hipStream_t st) {
+    const int64_t n16 = bytes / 16;
+    if (n16 <= 0 || wgs <= 0 || (copy && !dst) || (!copy && !sink)) return hipErrorInvalidValue;
+    const dim3 g((unsigned)wgs), b(256);
+    const u32x4* s = (const u32x4*)src;
+    if (copy) {
+        switch (unroll) {
+            case 4: launch_kernel(k_copy_probe<4>, g, b, 0, st, s, (u32x4*)dst, n16); break;
+            case 8: launch_kernel(k_copy_probe<8>, g, b, 0, st, s, (u32x4*)dst, n16); break;
+            case 16: launch_kernel(k_copy_probe<16>, g, b, 0, st, s, (u32x4*)dst, n16); break;
+            default: return hipErrorInvalidValue;
+        }
+    } else {
+        switch (unroll) {
+            case 4: launch_kernel(k_read_probe<4>, g, b, 0, st, s, n16, sink); break;
+            case 8: launch_kernel(k_read_probe<8>, g, b, 0, st, s, n16, sink); break;
+            case 16: launch_kernel(k_read_probe<16>, g, b, 0, st, s, n16, sink); break;
+            default: return hipErrorInvalidValue;
+        }
+    }
+    return hipGetLastError();
+}
+
+}  // namespace bh

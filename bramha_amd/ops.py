@@ -169,3 +169,11 @@ def time_attn(plane, q, k, v, seq_off, seq_len, n_q, n_kv, head_dim, max_len, it
 
 def synchronize(plane):
     check(lib.bh_synchronize(plane.ctx), plane.ctx)
+
+
+def time_probe(plane, copy, nbytes, wgs, unroll, iters=20):
+    """Mean microseconds of one HBM probe launch (bh_time_probe): copy = False streams nbytes with
+    16-byte non-temporal loads, True copies them into a second buffer."""
+    us = ctypes.c_double()
+    check(lib.bh_time_probe(plane.ctx, 1 if copy else 0, nbytes, wgs, unroll, iters, ctypes.byref(us)), plane.ctx)
+    return us.value

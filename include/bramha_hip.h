@@ -176,6 +176,13 @@ int bh_time_attn(bh_ctx* ctx, const float* q, const void* k, const void* v, int 
                  const int64_t* seq_off, const int32_t* seq_len, int batch, int n_q, int n_kv, int head_dim,
                  int max_len, float* out, int iters, size_t rotate_bytes, double* us_per_launch);
 
+/* HBM bandwidth probe: a graph of `iters` launches that each stream a `bytes` buffer (larger than
+ * the 256 MB Infinity Cache, so every launch reads HBM) with 16-byte non-temporal loads (copy = 0),
+ * or copy it into a second buffer (copy = 1); wgs workgroups of 256 threads, `unroll` (4, 8 or 16)
+ * loads in flight per thread. Returns the mean microseconds per launch; the achievable read (copy)
+ * bandwidth is bytes (2 * bytes) / time. The buffers are allocated and freed by the call. */
+int bh_time_probe(bh_ctx* ctx, int copy, size_t bytes, int wgs, int unroll, int iters, double* us_per_launch);
+
 /* ------------------------------------------------------------ decoder model */
 typedef struct {
     int32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab;
@@ -235,7 +242,9 @@ float bh_sample_uniform(uint64_t seed, int slot, int pos);
 int bh_model_missing(bh_model* m, int* n_missing);
 /* (Re)start sequence `slot` with room for `capacity` KV rows (capacity <= max_context when
  * eviction is on). Slots take consecutive regions of the packed buffer; a slot reopened with
- * a capacity no larger than before keeps its region. Clears its repetition-penalty counts. */
+ * a capacity no larger than before keeps its region. Clears its repetition-penalty counts.
+ * A slot of the decode batch may be reopened for a new sequence; its batch entry must then be
+ * replaced (bh_model_decode_replace) before the next decode. */
 int bh_model_seq_open(bh_model* m, int slot, int64_t capacity);
 /* Run prompt tokens [0, n) of `slot` through the model at its next positions without logits
  * (the reference prefills all prompt tokens but the last, cpu_engine.rs:2586-2757). */
@@ -243,7 +252,9 @@ int bh_model_prefill(bh_model* m, int slot, const uint32_t* tokens, int n);
 /* Define the decode batch: batch entry b decodes slot slots[b], whose next input token is
  * first_tokens[b]. */
 int bh_model_decode_setup(bh_model* m, int batch, const int32_t* slots, const uint32_t* first_tokens);
-/* Replace batch entry b by `slot` with next input token `first_token` (ragged refill). */
+/* Replace batch entry b by `slot` with next input token `first_token` (ragged refill). When the
+ * new slot has the entry's old KV region (the same slot reopened with no larger capacity) the
+ * captured decode step is kept; otherwise it is captured again at the next decode. */
 int bh_model_decode_replace(bh_model* m, int b, int slot, uint32_t first_token);
 /* Run n_steps greedy decode steps over the batch (one token per entry per step: embedding,
  * layers, final norm, LM head, repetition penalty 1.15 over the entry's generated ids,

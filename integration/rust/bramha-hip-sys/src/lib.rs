@@ -132,6 +132,8 @@ extern "C" {
         kv_rows: i64, seq_off: *const i64, seq_len: *const i32, batch: c_int, n_q: c_int, n_kv: c_int,
         head_dim: c_int, max_len: c_int, out: *mut f32, iters: c_int, rotate_bytes: usize,
         us_per_launch: *mut f64) -> c_int;
+    pub fn bh_time_probe(ctx: *mut bh_ctx, copy: c_int, bytes: usize, wgs: c_int, unroll: c_int, iters: c_int,
+        us_per_launch: *mut f64) -> c_int;
     // ---- the device decoder (generate_cpu_inner_logits, cpu_engine.rs:2290-3064)
     pub fn bh_model_create(ctx: *mut bh_ctx, cfg: *const bh_model_config, out: *mut *mut bh_model) -> c_int;
     pub fn bh_model_destroy(m: *mut bh_model);

@@ -73,12 +73,14 @@ def test_tiny_long_prompt_crosses_prefill_chunks(plane):
     assert np.max(np.abs(olg - glg)) <= 1e-4 * max(1.0, np.abs(olg).max())
 
 
+@pytest.mark.parametrize("plen", [70, 41, 12])
 @pytest.mark.parametrize("wfmt", [Q4_G32, Q4_ROW])
-def test_tiny_4bit_prefill_mfma(plane, wfmt):
-    # 69 prefill tokens: MFMA passes of 32 + 32, then a 5-token VALU pass
+def test_tiny_4bit_prefill_mfma(plane, wfmt, plen):
+    # 69 prefill tokens: a 64-token tiled MFMA chunk, then a 5-token VALU pass; 40 and 11 tokens:
+    # one tiled MFMA launch per projection over a partial token tile
     cfg = tiny_cfg(wfmt, Q4_G32 if wfmt == Q4_G32 else F32, gqa7=True)
     om, gm = _pair(plane, cfg, seed=21)
-    p = prompt(70, cfg.vocab, seed=22)
+    p = prompt(plen, cfg.vocab, seed=22)
     oids, olg = om.generate(p, 8, want_logits=True)
     gids, glg = gm.generate(p, 8, want_logits=True)
     assert np.array_equal(oids, gids)
@@ -253,6 +255,39 @@ def test_ragged_batch_and_refill(plane):
         assert np.array_equal(got[:n], want), b
     want = om.generate(newp, 6)
     assert np.array_equal(ids_b[:len(want), 2], want)
+
+
+@pytest.mark.parametrize("kv_f16", [False, True])
+def test_refill_reopening_the_finished_slot(plane, kv_f16):
+    """A finished entry's own slot reopened for a new sequence (same region, so the captured decode
+    step with its static region offsets stays valid) and swapped in with decode_replace; decoding
+    without replacing it first is refused. Every sequence against the oracle."""
+    cfg = tiny_cfg(Q4_G32, Q4_G32, gqa7=True, max_seqs=4, kv_f16=kv_f16, kv_rows=4 * 128)
+    om, gm = _pair(plane, cfg, seed=17)
+    prompts = [prompt(n, cfg.vocab, seed=30 + n) for n in (5, 12, 30)]
+    for s, p in enumerate(prompts):
+        gm.seq_open(s, 96)
+        gm.prefill(s, p[:-1])
+    gm.decode_setup([0, 1, 2], [p[-1] for p in prompts])
+    ids_a, lg_a = gm.decode(6, want_logits=True)
+    newp = prompt(20, cfg.vocab, seed=99)
+    gm.seq_open(1, 96)  # entry 1's slot, same capacity: same region
+    with pytest.raises(Exception):
+        gm.decode(1)
+    gm.prefill(1, newp[:-1])
+    gm.decode_replace(1, 1, newp[-1])
+    ids_b, lg_b = gm.decode(8, want_logits=True)
+    for b, p in enumerate(prompts):
+        n_steps = 14 if b != 1 else 6
+        want, wl = om.generate(p, n_steps, want_logits=True)
+        got = np.concatenate([ids_a[:, b], ids_b[:, b]])[:n_steps] if b != 1 else ids_a[:, b]
+        glg = np.concatenate([lg_a[:, b], lg_b[:, b]])[:n_steps] if b != 1 else lg_a[:, b]
+        n = agreement(want, got[:len(want)], wl, glg[:len(want)])
+        assert n == len(want), b
+    want, wl = om.generate(newp, 8, want_logits=True)
+    n = agreement(want, ids_b[:len(want), 1], wl, lg_b[:len(want), 1])
+    assert n == len(want)
+    assert np.max(np.abs(lg_b[:n, 1] - wl[:n])) < 2e-2
 
 
 def test_graph_replay_matches_single_steps(plane):

@@ -101,10 +101,15 @@ def test_prefill_through_prefix_cache(plane, tmp_path, kv_f16):
     assert a.seq_len(0) == b.seq_len(0) == 39
     ka, va = a.kv_read(0, 0, 39)
     kb, vb = b.kv_read(0, 0, 39)
-    assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+    # the cached rows are the cold run's own rows; the 7 rows after them were computed by a
+    # 7-token pass instead of inside the 39-token one (another kernel, another summation order)
+    assert np.array_equal(ka[:, :32], kb[:, :32]) and np.array_equal(va[:, :32], vb[:, :32])
+    tol = (2e-3 if kv_f16 else 1e-5) * max(1.0, np.abs(ka).max(), np.abs(va).max())
+    assert np.abs(ka - kb).max() <= tol and np.abs(va - vb).max() <= tol
     ia, la = a.decode_setup([0], [p[-1]]) or a.decode(8, want_logits=True)
     ib, lb = b.decode_setup([0], [p[-1]]) or b.decode(8, want_logits=True)
-    assert np.array_equal(ia, ib) and np.array_equal(la, lb)
+    assert np.array_equal(ia, ib)
+    assert np.abs(la - lb).max() <= 1e-3 * max(1.0, np.abs(la).max())
 
 
 @pytest.mark.gpu
