@@ -17,6 +17,7 @@ SOURCES = [
     "csrc/k_gemv.hip",
     "csrc/k_gemm.hip",
     "csrc/k_prefill.hip",
+    "csrc/k_lmhead.hip",
     "csrc/k_attn.hip",
     "csrc/k_attn_o.hip",
     "csrc/k_ops.hip",

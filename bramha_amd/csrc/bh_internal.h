@@ -130,13 +130,19 @@ struct GemvArgs {
     KvView kv;
     // EPI_LMHEAD
     const int32_t* slot = nullptr;     // [batch]
-    const uint16_t* pen = nullptr;     // [slots][vocab] generated-id counts
+    const uint16_t* pen = nullptr;     // [n_slots][vocab] generated-id counts
+    int n_slots = 0;
     int vocab = 0;
     float* part_val = nullptr;         // [batch][tiles64]
     int32_t* part_idx = nullptr;
     // prefill passes (launch_gemm_pf): scratch of batch * C * 64 fp16 for the activations split
     // once into hi + lo (k_prefill.hip); null: every workgroup splits them itself
     uint16_t* xhl = nullptr;
+    // The same hi + lo split, token-major ([batch][N / 32][64] fp16, the order of k_split_act):
+    // EPI_RESNORM of the MFMA passes also stores xw_out split there (N % 32 == 0); the batched
+    // LM head (k_lmhead.hip) takes its activations from x_hl when set instead of splitting x.
+    uint16_t* xw_hl = nullptr;
+    const uint16_t* x_hl = nullptr;
 };
 
 // The arguments of tokens b0 .. b0 + n - 1 of `a`: every per-token pointer advanced by b0.
@@ -144,7 +150,7 @@ __host__ __device__ inline GemvArgs gemv_tokens(const GemvArgs& a0, int b0, int 
     GemvArgs a = a0;
     a.batch = n;
     a.x = a0.x + (int64_t)b0 * a0.ldx;
-    a.y = a0.y + (int64_t)b0 * a0.ldy;
+    a.y = a0.y ? a0.y + (int64_t)b0 * a0.ldy : nullptr;
     if (a0.xw_out) a.xw_out = a0.xw_out + (int64_t)b0 * a0.ldy;
     if (a0.ssq_in) a.ssq_in = a0.ssq_in + (int64_t)b0 * a0.ssq_tiles;
     if (a0.ssq_out) a.ssq_out = a0.ssq_out + (int64_t)b0 * a0.ssq_tiles;
@@ -152,6 +158,8 @@ __host__ __device__ inline GemvArgs gemv_tokens(const GemvArgs& a0, int b0, int 
     if (a0.boff) a.boff = a0.boff + b0;
     if (a0.slot) a.slot = a0.slot + b0;
     const int tiles64 = (a0.n_pad + 63) / 64;
+    if (a0.xw_hl) a.xw_hl = a0.xw_hl + (int64_t)b0 * (a0.N / 32) * 64;
+    if (a0.x_hl) a.x_hl = a0.x_hl + (int64_t)b0 * a0.C * 64;
     if (a0.part_val) a.part_val = a0.part_val + (int64_t)b0 * tiles64;
     if (a0.part_idx) a.part_idx = a0.part_idx + (int64_t)b0 * tiles64;
     return a;
@@ -180,6 +188,10 @@ hipError_t launch_gemm_mf(int fmt, int epi, const GemvArgs& a, int B, int rw, hi
 // MFMA GEMM over all a.batch tokens at once for prefill chunks (k_prefill.hip): 128-row by
 // 128-token tiles (64 tokens for the gate/up pair). Not for EPI_LMHEAD.
 hipError_t launch_gemm_pf(int fmt, int epi, const GemvArgs& a, hipStream_t st);
+// LM head of 1..32 tokens over a Q4_G32 matrix, about one workgroup per CU with the activations
+// in LDS (k_lmhead.hip); lmhead_mf_fits tells whether a pass's shape is within its limits.
+bool lmhead_mf_fits(const GemvArgs& a, int n_cu);
+hipError_t launch_lmhead_mf(const GemvArgs& a, int n_cu, hipStream_t st);
 constexpr int PF_MIN_TOKENS = 64;  // launch_gemv hands passes of at least this many tokens to it
 // Workgroups per row tile for a K-split GEMV over `tiles` row tiles and C chunks.
 int gemv_splits(int tiles, int C, int min_chunks, int target);

@@ -68,6 +68,7 @@ struct bh_model {
     size_t attn_rows = 0;          // query rows of attn_part
     float* split_part = nullptr;   // K-split sums of split projections
     uint16_t* xhl = nullptr;       // prefill passes: activations split into fp16 hi + lo
+    uint16_t* xw_hl = nullptr;     // decode: final-norm activations split for the batched LM head
     int32_t* split_cnt = nullptr;  // their per-tile arrival counters (zero when idle)
     // decode batch state (read by the captured graph) and prefill staging, kept apart so a
     // prefill between decode calls leaves the batch intact
@@ -97,6 +98,8 @@ struct bh_model {
     hipGraph_t graph = nullptr;
     hipGraphExec_t gexec = nullptr;
     int g_B = 0, g_splits = 0, g_rows = 0;
+    bool store_logits = false;  // the next forward stores raw logits
+    bool g_logits = false;      // the captured step stores raw logits
     std::vector<int64_t> g_off;    // region offsets the captured step holds as launch arguments
     int64_t g_cap = 0;             // and the smallest region capacity it assumes
 
@@ -188,6 +191,16 @@ void weight_args(bh_model* m, GemvArgs& a, const DevWeight& w) {
     a.xhl = m->xhl;
 }
 
+// Whether the last down projection of a decode step over M tokens also stores the final-norm
+// activations split into fp16 hi + lo for the LM head: every pass of M (launch_gemv) is then an
+// MFMA pass on both sides (4-bit weights, 9..32 tokens; a remainder of at most 8 tokens takes
+// the VALU passes on both sides, which neither store nor read the split).
+static bool lm_presplit(const bh_model* m, int M) {
+    const bh_model_config& c = m->c;
+    return m->xw_hl && M > 8 && M < PF_MIN_TOKENS && c.head_fmt == BH_Q4_G32 && c.hidden % 32 == 0 &&
+           (c.wfmt == BH_Q4_G32 || c.wfmt == BH_Q4_ROW);
+}
+
 // One forward pass over M tokens whose residual stream (x, xw, ssq) holds their embedding rows:
 // the decode batch (decode = true: logits, penalty, argmax and the next step's stream) or a
 // staged prefill chunk.
@@ -274,16 +287,21 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
         d.ldx = I;
         d.batch = M;
         stream_output(m, d, l + 1 < c.n_layers ? m->L[l + 1].ln1 : m->norm);  // final norm after the last layer
+        if (decode && l + 1 == c.n_layers && lm_presplit(m, M)) d.xw_hl = m->xw_hl;
         e = timed(m, BH_K_GEMV_DOWN, [&] { return launch_gemv(c.wfmt, EPI_RESNORM, d, st); });
     }
     if (e != hipSuccess || !decode) return e;
     GemvArgs lm;
     weight_args(m, lm, m->have_lm_head ? m->lm_head : m->embed);
     stream_input(m, lm);
-    lm.y = m->logits;
+    // raw logits are stored only for a caller that asked for them and for top-k sampling, which
+    // reads them; the greedy step needs only the per-tile partials
+    lm.y = (m->store_logits || m->temperature > 0.f) ? m->logits : nullptr;
     lm.ldy = c.vocab;
     lm.batch = M;
     lm.pen = m->d_pen;
+    lm.n_slots = c.max_seqs;
+    if (lm_presplit(m, M)) lm.x_hl = m->xw_hl;
     lm.vocab = c.vocab;
     lm.slot = slot;
     lm.part_val = m->part_val;
@@ -498,6 +516,7 @@ int bh_model_create(bh_ctx* ctx, const bh_model_config* cfg, bh_model** out) {
         {(void**)&m->d_pboff, T * 8},
         {(void**)&m->d_ids, (size_t)m->ids_steps * DB * 4},
         {(void**)&m->d_pen, (size_t)c.max_seqs * c.vocab * 2},
+        {(void**)&m->xw_hl, DB * c.hidden * 4},
     };
     for (auto& b : bufs)
         if ((e = dmalloc(m, b.p, b.bytes)) != hipSuccess) return bail(e, "hipMalloc(activations)");
@@ -842,7 +861,8 @@ static int decode_locked(bh_model* m, int n_steps, uint32_t* ids_out, float* raw
     int splits, rows;
     attn_plan(decode_len_bound(m, n_steps), m->B, m->c.n_kv_heads, m->c.head_dim, &splits, &rows);
     hipError_t e = hipSuccess;
-    if (!m->gexec || m->g_B != m->B || m->g_splits != splits || m->g_rows != rows) {
+    m->store_logits = raw_logits != nullptr;
+    if (!m->gexec || m->g_B != m->B || m->g_splits != splits || m->g_rows != rows || m->g_logits != m->store_logits) {
         drop_graph(m);
         e = hipStreamBeginCapture(m->st, hipStreamCaptureModeThreadLocal);
         if (e != hipSuccess) return m->ctx->hip_fail(e, "hipStreamBeginCapture");
@@ -857,6 +877,7 @@ static int decode_locked(bh_model* m, int n_steps, uint32_t* ids_out, float* raw
         m->g_B = m->B;
         m->g_splits = splits;
         m->g_rows = rows;
+        m->g_logits = m->store_logits;
         m->g_off.resize(m->B);
         m->g_cap = INT64_MAX;
         for (int b = 0; b < m->B; ++b) {
@@ -951,6 +972,7 @@ int bh_model_time_kernels(bh_model* m, int n_steps, double* mean_us, int64_t* la
     std::vector<double> tot(BH_K_COUNT, 0.0);
     std::vector<int64_t> cnt(BH_K_COUNT, 0);
     hipError_t e = decode_start(m);
+    m->store_logits = false;  // the greedy step as bh_model_decode runs it without raw logits
     for (int s = 0; s < n_steps && e == hipSuccess; ++s) {
         m->timing = true;
         m->recs.clear();
@@ -991,8 +1013,10 @@ int bh_model_kernel_bytes(bh_model* m, int kclass, double* bytes) {
             return BH_OK;
         case BH_K_GEMV_GATEUP: *bytes = weight_bytes(w.gate) + weight_bytes(w.up) + B * (H + T) * 4 + B * I * 4; return BH_OK;
         case BH_K_GEMV_DOWN: *bytes = weight_bytes(w.down) + B * I * 4 + B * (3 * H + T) * 4 + H * 4; return BH_OK;
-        case BH_K_LM_HEAD:  // tied table, xw in; logits out, penalty counts read
-            *bytes = weight_bytes(m->have_lm_head ? m->lm_head : m->embed) + B * (H + T) * 4 + B * (double)c.vocab * 4 + B * (double)c.vocab * 2;
+        case BH_K_LM_HEAD:  // tied table, xw in, penalty counts read; raw logits out when the greedy
+                            // step stores them (top-k sampling)
+            *bytes = weight_bytes(m->have_lm_head ? m->lm_head : m->embed) + B * (H + T) * 4 + B * (double)c.vocab * 2 +
+                     (m->temperature > 0.f ? B * (double)c.vocab * 4 : 0.0);
             return BH_OK;
         case BH_K_ATTN:
         case BH_K_ATTN_O: {

@@ -12,6 +12,10 @@
 
 namespace bh {
 
+// Workgroup barrier for data exchanged through LDS only: waits for this wave's LDS operations,
+// not for its outstanding global loads and stores (__syncthreads() also waits for those).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // Per-row factor applied after the sum (row formats); 1 for F32 and Q4_G32.
 template <int FMT>
 __device__ __forceinline__ float row_scale(const void* S, int64_t n) {
@@ -213,14 +217,14 @@ __device__ __forceinline__ bool split_reduce_wave(const GemvArgs& a, float& sum,
     return true;
 }
 
-// LM-head element of token b, row nn: the raw logit is stored, then the repetition penalty
+// LM-head element of token b, row nn: the raw logit is stored (when y is set), then the repetition penalty
 // (cpu_engine.rs:2984-2992) applied `cnt` times; -inf for rows past the vocabulary, tokens past
 // the batch and NaN (the first-max scan uses `>`, so NaN never wins).
 template <int FMT>
 __device__ __forceinline__ float lm_elem(const GemvArgs& a, float f, int b, int64_t nn, const float* rn, int cnt) {
     if (nn >= a.N || b >= a.batch) return -INFINITY;
     float v = f * row_scale<FMT>(a.S, nn) * rn[b];
-    a.y[(int64_t)b * a.ldy + nn] = v;
+    if (a.y) a.y[(int64_t)b * a.ldy + nn] = v;
     for (int t = 0; t < cnt; ++t) v = v > 0.f ? v / 1.15f : v * 1.15f;
     return v > -INFINITY ? v : -INFINITY;
 }
@@ -311,8 +315,18 @@ __device__ __forceinline__ void run_resnorm_pre(const GemvArgs& a, const float* 
             float o = fin[i] * row_scale<FMT>(a.S, nn);
             if (a.bias) o += rp.bias[k];
             const float v = rp.x0[k] + o;
+            const float xw = v * rp.w1[k];
             a.y[(int64_t)b * a.ldy + nn] = v;
-            a.xw_out[(int64_t)b * a.ldy + nn] = v * rp.w1[k];
+            a.xw_out[(int64_t)b * a.ldy + nn] = xw;
+            if (a.xw_hl) {  // element nn of chunk nn / 32 sits at K slot kperm^-1(nn % 8) of its 8
+                const int q = (int)(nn & 31), e = q & 7;
+                const int slot = (((e & 3) ^ 1) << 1) | (e >> 2);
+                const _Float16 h = (_Float16)xw;
+                const _Float16 l = (_Float16)(xw - (float)h);
+                uint16_t* d = a.xw_hl + ((int64_t)b * (a.N / 32) + (nn >> 5)) * 64 + (q >> 3) * 8 + slot;
+                d[0] = __builtin_bit_cast(uint16_t, h);
+                d[32] = __builtin_bit_cast(uint16_t, l);
+            }
             sq = v * v;
         }
         scratch[i] = sq;

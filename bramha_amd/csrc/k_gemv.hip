@@ -15,6 +15,8 @@
 
 #include <hip/hip_fp16.h>
 
+#include <atomic>
+
 #include "k_epilogue.h"
 #include "k_stream.h"
 
@@ -199,6 +201,19 @@ static int auto_splits(const GemvArgs& a, bool mfma, int rows_per_tile, int tot)
     return ksw;
 }
 
+// Compute units of the current device (queried once per device).
+static int device_cus() {
+    static std::atomic<int> cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int v = cus[dev].load(std::memory_order_relaxed);
+    if (v <= 0) {
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        cus[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
+
 // Splits the batch into passes: MFMA passes of 32 or 16 rows for 4-bit weights (k_gemm.hip),
 // VALU passes of at most 8 rows otherwise.
 hipError_t launch_gemv(int fmt, int epi, const GemvArgs& a0, hipStream_t st) {
@@ -226,7 +241,9 @@ hipError_t launch_gemv(int fmt, int epi, const GemvArgs& a0, hipStream_t st) {
         const int B = mf ? (rem > 16 ? 32 : 16) : (rem >= 8 ? 8 : (rem >= 4 ? 4 : (rem >= 2 ? 2 : 1)));
         GemvArgs a = gemv_tokens(a0, b0, mf ? std::min(B, rem) : B);
         hipError_t e;
-        if (mf) {
+        if (mf && epi == EPI_LMHEAD && fmt == BH_Q4_G32 && lmhead_mf_fits(a, device_cus())) {
+            e = launch_lmhead_mf(a, device_cus(), st);
+        } else if (mf) {
             a.ksw = auto_splits(a0, true, 64 * rw, nacc * B * 64 * rw);
             e = launch_gemm_mf(fmt, epi, a, B, rw, st);
         } else {

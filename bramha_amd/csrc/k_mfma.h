@@ -34,6 +34,28 @@ __device__ __forceinline__ half8 dec8(uint32_t w) {
     return r;
 }
 
+// dec8 at 11 VALU operations per dword instead of 15: each pair is one v_and_or_b32 (mask in an
+// SGPR, 0x64006400 in the VGPR `mg` of dec8_magic(), which the caller holds across its loop; gfx9
+// VOP3 encodings take neither two scalar operands nor a literal) after the shift.
+__device__ __forceinline__ uint32_t dec8_magic() {
+    uint32_t r;
+    asm("v_mov_b32 %0, 0x64006400" : "=v"(r));
+    return r;
+}
+__device__ __forceinline__ half8 dec8(uint32_t w, uint32_t mg) {
+    const half2v off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+    half8 r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        uint32_t p;
+        asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(p) : "v"(w >> (4 * j)), "s"(0x000F000Fu), "v"(mg));
+        const half2v h = __builtin_bit_cast(half2v, p) + off;
+        r[2 * j] = h.x;
+        r[2 * j + 1] = h.y;
+    }
+    return r;
+}
+
 // f32 activations -> fp16 hi + lo (hi + lo carries ~22 bits of the f32 mantissa).
 __device__ __forceinline__ void split8(const float4& x0, const float4& x1, half8& hi, half8& lo) {
     const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};

@@ -259,7 +259,8 @@ int bh_model_decode_replace(bh_model* m, int b, int slot, uint32_t first_token);
 /* Run n_steps greedy decode steps over the batch (one token per entry per step: embedding,
  * layers, final norm, LM head, repetition penalty 1.15 over the entry's generated ids,
  * first-max argmax; cpu_engine.rs:2819-3034). ids_out (host, optional): [n_steps][batch].
- * raw_logits (host, optional): [n_steps][batch][vocab] logits before the penalty.
+ * raw_logits (host, optional): [n_steps][batch][vocab] logits before the penalty. Without it the
+ * greedy step keeps the logits on chip (per-tile maxima only).
  * Steps are replayed from a captured HIP graph; the call returns when they are done. */
 int bh_model_decode(bh_model* m, int n_steps, uint32_t* ids_out, float* raw_logits);
 /* The reference's generate loop at temperature 0 for one sequence: open `slot`, prefill
@@ -274,7 +275,9 @@ void* bh_model_stream(bh_model* m);
  * events at the kernel's own start and end on the model's stream. Returns the mean duration in
  * microseconds and the launch count per class. (BH_K_NORM has no launches: the RMSNorm is folded
  * into the projections. BH_K_ATTN_O is the batch-1 decode launch that computes the attention, the
- * O projection and the residual add together; where it runs, BH_K_ATTN and BH_K_GEMV_O do not.) */
+ * O projection and the residual add together; where it runs, BH_K_ATTN and BH_K_GEMV_O do not.)
+ * The steps are those of bh_model_decode without raw_logits: the LM head stores raw logits only
+ * under top-k sampling. */
 enum { BH_K_GEMV_QKV = 0, BH_K_ATTN = 1, BH_K_GEMV_O = 2, BH_K_GEMV_GATEUP = 3, BH_K_GEMV_DOWN = 4,
        BH_K_LM_HEAD = 5, BH_K_NORM = 6, BH_K_OTHER = 7, BH_K_ATTN_O = 8, BH_K_COUNT = 9 };
 int bh_model_time_kernels(bh_model* m, int n_steps, double* mean_us /*[BH_K_COUNT]*/,
