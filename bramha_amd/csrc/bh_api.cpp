@@ -345,7 +345,7 @@ int bh_init(int device, bh_ctx** out) {
         return BH_ERR_HIP;
     }
     // split scratch up front, so that no GEMV call (captured or not) allocates
-    const size_t pb = (size_t)SPLIT_WG_MAX * SPLIT_TOT_MAX * 4, cb = (size_t)SPLIT_WG_MAX * 4;
+    const size_t pb = (size_t)SPLIT_PART_FLOATS * 4, cb = (size_t)SPLIT_TILES_MAX * 4;
     if (hipMalloc(&c->split_part, pb) != hipSuccess || hipMalloc(&c->split_cnt, cb) != hipSuccess ||
         hipMemset(c->split_cnt, 0, cb) != hipSuccess) {
         if (c->split_part) hipFree(c->split_part);

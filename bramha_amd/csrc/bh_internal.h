@@ -200,8 +200,9 @@ constexpr int MAX_KSW = 16;
 // weights of at least STREAM_BYTES packed bytes.
 constexpr int CPOL_STREAM = 2;
 constexpr size_t STREAM_BYTES = 16u << 20;
-constexpr int SPLIT_WG_MAX = 512;   // tiles * ksw of a split launch
 constexpr int SPLIT_TOT_MAX = 2 * 32 * 128;  // NACC * B * ROWS floats per workgroup
+constexpr int64_t SPLIT_PART_FLOATS = (int64_t)512 * SPLIT_TOT_MAX;  // split sums of one launch
+constexpr int SPLIT_TILES_MAX = 4096;  // arrival counters: row tiles (times token groups) of one launch
 
 // k_ops.hip
 hipError_t launch_rmsnorm(const float* x, const float* w, float eps, float* out, int rows, int n, hipStream_t st);

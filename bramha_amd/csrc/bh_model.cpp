@@ -503,8 +503,8 @@ int bh_model_create(bh_ctx* ctx, const bh_model_config* cfg, bh_model** out) {
         {(void**)&m->part_idx, DB * m->tiles_lm * 4},
         {(void**)&m->attn_part, m->attn_rows * c.n_heads * m->max_splits * (c.head_dim + 2) * 4},
         {(void**)&m->attn_cnt, T * c.n_kv_heads * 4},
-        {(void**)&m->split_part, (size_t)SPLIT_WG_MAX * SPLIT_TOT_MAX * 4},
-        {(void**)&m->split_cnt, (size_t)4096 * 4},
+        {(void**)&m->split_part, (size_t)SPLIT_PART_FLOATS * 4},
+        {(void**)&m->split_cnt, (size_t)SPLIT_TILES_MAX * 4},
         {(void**)&m->d_tok, T * 4},
         {(void**)&m->d_pos, T * 4},
         {(void**)&m->d_slot, T * 4},

@@ -286,7 +286,7 @@ hipError_t launch_gemm_mf(int fmt, int epi, const GemvArgs& a, int B, int rw, hi
     const int tiles = (a.n_pad + 64 * rw - 1) / (64 * rw);
     const int tot16 = (epi == EPI_SILU ? 2 : 1) * 16 * 64 * rw;
     if (B == 32 && a.batch > 16 && epi != EPI_LMHEAD && 2 * tiles * a.ksw <= 512 &&
-        (a.ksw == 1 || (2 * tiles <= SPLIT_WG_MAX && (int64_t)2 * tiles * a.ksw * tot16 <= (int64_t)SPLIT_WG_MAX * SPLIT_TOT_MAX))) {
+        (a.ksw == 1 || (2 * tiles <= SPLIT_TILES_MAX && (int64_t)2 * tiles * a.ksw * tot16 <= SPLIT_PART_FLOATS))) {
         groups = 2;
         B = 16;
     }

@@ -169,7 +169,9 @@ static int waves_per_tile(int tiles, int rw, int C, int nacc, int B) {
     // matrices with many row tiles, so that every workgroup of the launch stays resident (18944 x
     // 3584 streams 2.8 TB/s instead of 2.3 with 16; the 7B gate/up pair 25 us instead of 31);
     // 16 on small ones (latency-bound: 16 waves per tile are fastest on 4864 x 896)
-    ks = std::max(1, std::min({ks, (tiles > 128 ? (nacc == 2 ? 8 : 12) : 16) / rw, std::max(1, C / 2)}));
+    // (a K-split launch of at most 256 workgroups keeps 16: 3584 x 18944 at 4 splits, 13.3 us
+    // instead of 14.8 with 12)
+    ks = std::max(1, std::min({ks, (tiles > 256 ? (nacc == 2 ? 8 : 12) : 16) / rw, std::max(1, C / 2)}));
     while (ks > 1 && (size_t)ks * nacc * B * 64 * rw * 4 > 60 * 1024) --ks;
     return ks;
 }
@@ -182,22 +184,27 @@ int gemv_splits(int tiles, int C, int min_chunks, int target) {
 }
 
 // K splits of one pass when the caller left the choice to the launcher (ksw == 0) and provided
-// split scratch: VALU passes split only long-K matrices with few row tiles; MFMA passes split
-// whenever the row tiles leave CUs idle. Bounded by the scratch (SPLIT_WG_MAX workgroups of
-// SPLIT_TOT_MAX floats).
-static int auto_splits(const GemvArgs& a, bool mfma, int rows_per_tile, int tot) {
+// split scratch: VALU passes split long-K matrices with few row tiles, and at batch 1 also long-K
+// matrices with many (16 chunks per workgroup); MFMA passes split whenever the row tiles leave
+// CUs idle. Bounded by the scratch (SPLIT_PART_FLOATS floats of sums, SPLIT_TILES_MAX arrival
+// counters).
+static int auto_splits(const GemvArgs& a, int epi, bool mfma, int rows_per_tile, int tot) {
     if (a.ksw > 0) return a.ksw;
     if (!a.part || !a.tile_cnt || tot > SPLIT_TOT_MAX) return 1;
     const int tiles = (a.n_pad + rows_per_tile - 1) / rows_per_tile;
+    if (tiles > SPLIT_TILES_MAX) return 1;
     int ksw;
     // splits pay for their ordered reduction only on long-K matrices (measured: the 896-wide
     // projections are fastest unsplit at 1 and at 32 tokens; the 3584- and 18944-wide ones of a
     // 7B model stream 1.3-2x faster split to fill the CUs); MFMA passes aim at two workgroups
-    // per CU, VALU passes at one
-    ksw = !(a.C >= 64) ? 1
-          : mfma ? (tiles < 256 ? gemv_splits(tiles, a.C, 16, 512) : 1)
-                 : (tiles < 128 ? std::min(gemv_splits(tiles, a.C, 16, 256), 8) : 1);
-    while (ksw > 1 && tiles * ksw > SPLIT_WG_MAX) --ksw;
+    // per CU, VALU passes at one. A batch-1 pass over many row tiles and a long K (the 7B
+    // 18944 x 3584 gate/up pair: 25.2 us unsplit, 23.2 at 7 splits, 24.4 at 2, 26.9 at 14) takes
+    // 16-chunk splits; not the LM head, whose split would add a reduction to its argmax epilogue.
+    if (!(a.C >= 64)) ksw = 1;
+    else if (mfma) ksw = tiles < 256 ? gemv_splits(tiles, a.C, 16, 512) : 1;
+    else if (tiles < 128) ksw = std::min(gemv_splits(tiles, a.C, 16, 256), 8);
+    else ksw = (a.batch == 1 && a.C >= 100 && epi != EPI_LMHEAD) ? std::min(a.C / 16, 8) : 1;
+    while (ksw > 1 && (int64_t)tiles * ksw * tot > (int64_t)SPLIT_PART_FLOATS) --ksw;
     return ksw;
 }
 
@@ -244,10 +251,10 @@ hipError_t launch_gemv(int fmt, int epi, const GemvArgs& a0, hipStream_t st) {
         if (mf && epi == EPI_LMHEAD && fmt == BH_Q4_G32 && lmhead_mf_fits(a, device_cus())) {
             e = launch_lmhead_mf(a, device_cus(), st);
         } else if (mf) {
-            a.ksw = auto_splits(a0, true, 64 * rw, nacc * B * 64 * rw);
+            a.ksw = auto_splits(a0, epi, true, 64 * rw, nacc * B * 64 * rw);
             e = launch_gemm_mf(fmt, epi, a, B, rw, st);
         } else {
-            a.ksw = auto_splits(a0, false, 64 * rw, nacc * B * 64 * rw);
+            a.ksw = auto_splits(a0, epi, false, 64 * rw, nacc * B * 64 * rw);
             const int tiles = (a0.n_pad + 64 * rw - 1) / (64 * rw);
             const int ks = waves_per_tile(tiles * a.ksw, rw, (a0.C + a.ksw - 1) / a.ksw, nacc, B);
             const int cpw = ((a0.C + a.ksw - 1) / a.ksw + ks - 1) / ks;  // chunks per wave
