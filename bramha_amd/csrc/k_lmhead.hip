@@ -104,7 +104,7 @@ __device__ __forceinline__ void lh_sweep(const GemvArgs& a, const LhCtx& k, cons
     };
 
     static_assert(RB <= 5, "a sweep spans at most two 64-row tiles");
-    const uint32_t mg = dec8_magic();
+    const Dec8K mg = dec8_consts();
     f32x4 acc[RB][TB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)

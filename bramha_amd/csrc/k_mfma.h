@@ -34,21 +34,23 @@ __device__ __forceinline__ half8 dec8(uint32_t w) {
     return r;
 }
 
-// dec8 at 11 VALU operations per dword instead of 15: each pair is one v_and_or_b32 (mask in an
-// SGPR, 0x64006400 in the VGPR `mg` of dec8_magic(), which the caller holds across its loop; gfx9
-// VOP3 encodings take neither two scalar operands nor a literal) after the shift.
-__device__ __forceinline__ uint32_t dec8_magic() {
-    uint32_t r;
-    asm("v_mov_b32 %0, 0x64006400" : "=v"(r));
-    return r;
+// dec8 at 11 VALU operations per dword instead of 15: each pair is one v_and_or_b32 after the
+// shift. gfx9 VOP3 encodings take no literal, so with both constants literal the compiler emits a
+// separate AND and OR; with 0x64006400 held in a VGPR it cannot fold (plus a lane count that is
+// always zero), computed once by the caller and kept across its loop, it selects v_and_or_b32
+// with the mask in an SGPR.
+struct Dec8K {
+    uint32_t magic;
+};
+__device__ __forceinline__ Dec8K dec8_consts() {
+    return Dec8K{0x64006400u + __builtin_amdgcn_mbcnt_lo(0u, 0u)};
 }
-__device__ __forceinline__ half8 dec8(uint32_t w, uint32_t mg) {
+__device__ __forceinline__ half8 dec8(uint32_t w, const Dec8K& k) {
     const half2v off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
     half8 r;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        uint32_t p;
-        asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(p) : "v"(w >> (4 * j)), "s"(0x000F000Fu), "v"(mg));
+        const uint32_t p = ((w >> (4 * j)) & 0x000F000Fu) | k.magic;
         const half2v h = __builtin_bit_cast(half2v, p) + off;
         r[2 * j] = h.x;
         r[2 * j + 1] = h.y;
