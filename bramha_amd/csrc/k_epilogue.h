@@ -331,7 +331,7 @@ __device__ __forceinline__ void run_resnorm_pre(const GemvArgs& a, const float* 
         }
         scratch[i] = sq;
     }
-    __syncthreads();
+    lds_barrier();  // LDS scratch only: the stores above need not complete
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     constexpr int SUB = ROWS / 64;
     for (int q = wave; q < B * SUB; q += NT / 64) {
@@ -351,7 +351,7 @@ __device__ __forceinline__ void run_lmhead_pre(const GemvArgs& a, const float* f
         const int i = threadIdx.x + k * NT;
         if (i < B * ROWS) scratch[i] = lm_elem<FMT>(a, fin[i], i / ROWS, row0 + i % ROWS, rn, (int)pp.c[k]);
     }
-    __syncthreads();
+    lds_barrier();  // LDS scratch only: the stores above need not complete
     lm_argmax<B, ROWS>(a, scratch, row0);
 }
 
@@ -490,7 +490,7 @@ __device__ __forceinline__ void run_epilogue(const GemvArgs& a, const float* fin
                 if (ok) qkv_row<FMT>(a, nn, fin[rr], fin[rr + qkv_partner(a, nn)], rn[0], *pre);
             } else if constexpr (EPI == EPI_LMHEAD) {
                 if (rr < ROWS) scratch[rr] = lm_elem<FMT>(a, fin[rr], 0, nn, rn, pre->cnt);
-                __syncthreads();
+                lds_barrier();  // LDS scratch only: the stores above need not complete
                 lm_argmax<1, ROWS>(a, scratch, row0);
             }
             return;
@@ -526,7 +526,7 @@ __device__ __forceinline__ void run_epilogue(const GemvArgs& a, const float* fin
             }
             scratch[i] = sq;
         }
-        __syncthreads();
+        lds_barrier();  // LDS scratch only: the stores above need not complete
         constexpr int SUB = ROWS / 64;
         for (int q = wave; q < B * SUB; q += nwaves) {
             const int b = q / SUB, sub = q % SUB;
@@ -583,7 +583,7 @@ __device__ __forceinline__ void run_epilogue(const GemvArgs& a, const float* fin
             const int cnt = (nn < a.N && b < a.batch) ? a.pen[(int64_t)a.slot[b] * a.vocab + nn] : 0;
             scratch[i] = lm_elem<FMT>(a, fin[i], b, nn, rn, cnt);
         }
-        __syncthreads();
+        lds_barrier();  // LDS scratch only: the stores above need not complete
         lm_argmax<B, ROWS>(a, scratch, row0);
     }
 }

@@ -234,7 +234,6 @@ __global__ void __launch_bounds__(64 * KW * RW) k_gemm_mf(const GemvArgs a0) {
 // Waves per row group: 8 for passes of at most 512 workgroups, whose time is the chain of loads
 // each wave walks (896 x 4864 at 32 tokens: 17.7 -> 13.8 us; 896-wide K unchanged), 4 for larger
 // ones, where occupancy decides (the 151936-row LM head at 32 tokens: 66 us with 4, 103 with 8).
-// One chunk per stage: two-chunk stages measured slower at every shape.
 template <int FMT, int B, int EPI, int RW, int KW>
 hipError_t launch_k(const GemvArgs& a, int groups, hipStream_t st) {
     constexpr int NACC = EPI == EPI_SILU ? 2 : 1;
@@ -242,7 +241,15 @@ hipError_t launch_k(const GemvArgs& a, int groups, hipStream_t st) {
     const int tiles = (a.n_pad + ROWS - 1) / ROWS;
     const size_t shm = (32 + (size_t)NACC * B * ROWS + (size_t)std::max(1, KW / 2) * B * (ROWS + 4)) * sizeof(float);
     if (shm > 64 * 1024) return hipErrorInvalidValue;
-    launch_kernel((k_gemm_mf<FMT, B, EPI, RW, KW, 1>), dim3(tiles * a.ksw, groups), dim3(64 * KW * RW), shm, st, a);
+    // 8-wave launches without a K split over workgroups take two chunks per stage (all of a
+    // 3.5-chunk wave's loads in flight at once: 896-wide K at 32 tokens, QKV 10.4 -> 10.0 us, O
+    // 9.4 -> 8.7, gate/up 13.1 -> 12.6); split launches keep one (down 11.5 -> 11.9 with two)
+    // (not the 32-token gate/up pair, whose two-chunk stages do not fit the registers)
+    constexpr bool S2 = KW == 8 && !(NACC == 2 && B == 32);
+    if (S2 && a.ksw == 1)
+        launch_kernel((k_gemm_mf<FMT, B, EPI, RW, KW, S2 ? 2 : 1>), dim3(tiles * a.ksw, groups), dim3(64 * KW * RW), shm, st, a);
+    else
+        launch_kernel((k_gemm_mf<FMT, B, EPI, RW, KW, 1>), dim3(tiles * a.ksw, groups), dim3(64 * KW * RW), shm, st, a);
     return hipGetLastError();
 }
 
