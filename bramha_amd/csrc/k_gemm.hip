@@ -283,8 +283,21 @@ hipError_t launch_e(int epi, const GemvArgs& a, int B, int groups, int rw, hipSt
 }  // namespace
 
 hipError_t launch_gemm_mf(int fmt, int epi, const GemvArgs& a, int B, int rw, hipStream_t st) {
-    if ((B != 16 && B != 32) || a.batch < 1 || a.batch > B || a.ksw < 1 || a.n_pad % 64 || rw < 1 || rw > 2)
+    if ((B != 16 && B != 32 && B != 48 && B != 64) || a.batch < 1 || a.batch > B || a.ksw < 1 || a.n_pad % 64 ||
+        rw < 1 || rw > 2 || (B > 32 && (epi == EPI_LMHEAD || a.batch <= B - 16)))
         return hipErrorInvalidValue;
+    if (B > 32) {
+        // 33..64 tokens (a short prefill chunk: a refill's prompt): B / 16 groups of 16 tokens in
+        // one launch, each group its own split scratch region, every group holding a token
+        const int groups = B / 16;
+        const int tiles = (a.n_pad + 64 * rw - 1) / (64 * rw);
+        const int tot16 = (epi == EPI_SILU ? 2 : 1) * 16 * 64 * rw;
+        if (a.ksw > 1 && (groups * tiles > SPLIT_TILES_MAX || (int64_t)groups * tiles * a.ksw * tot16 > SPLIT_PART_FLOATS))
+            return hipErrorInvalidValue;
+        if (fmt == BH_Q4_G32) return launch_e<BH_Q4_G32>(epi, a, 16, groups, rw, st);
+        if (fmt == BH_Q4_ROW) return launch_e<BH_Q4_ROW>(epi, a, 16, groups, rw, st);
+        return hipErrorInvalidValue;
+    }
     // A 32-token pass whose launch leaves most CUs idle runs as two 16-token groups: twice the
     // workgroups with no reduction between them (a 16-token pass of 896 x 896 takes 7.7 us, a
     // 32-token one 10.2). Not for the LM head, whose row tiles fill the chip and whose weights

@@ -245,13 +245,20 @@ hipError_t launch_gemv(int fmt, int epi, const GemvArgs& a0, hipStream_t st) {
         // next column count up with only its tokens valid (activations past them read as zero,
         // nothing of theirs is stored), so a pass of 9..31 tokens is one launch
         const bool mf = q4 && rem > 8;
-        const int B = mf ? (rem > 16 ? 32 : 16) : (rem >= 8 ? 8 : (rem >= 4 ? 4 : (rem >= 2 ? 2 : 1)));
+        int B = mf ? (rem > 16 ? 32 : 16) : (rem >= 8 ? 8 : (rem >= 4 ? 4 : (rem >= 2 ? 2 : 1)));
+        // 33..63 tokens (below the tiled prefill GEMM): one launch of 16-token groups instead of
+        // two 32-token passes (a 63-token refill prompt: one dependent launch per projection)
+        if (mf && rem > 32 && epi != EPI_LMHEAD) B = (rem + 15) / 16 * 16;
         GemvArgs a = gemv_tokens(a0, b0, mf ? std::min(B, rem) : B);
         hipError_t e;
         if (mf && epi == EPI_LMHEAD && fmt == BH_Q4_G32 && lmhead_mf_fits(a, device_cus())) {
             e = launch_lmhead_mf(a, device_cus(), st);
         } else if (mf) {
-            a.ksw = auto_splits(a0, epi, true, 64 * rw, nacc * B * 64 * rw);
+            a.ksw = auto_splits(a0, epi, true, 64 * rw, nacc * std::min(B, 32) * 64 * rw);
+            if (B > 32 && a.ksw > 1) {  // the groups' split scratch must fit too
+                const int64_t gt = (int64_t)(B / 16) * ((a0.n_pad + 64 * rw - 1) / (64 * rw));
+                if (gt > SPLIT_TILES_MAX || gt * a.ksw * nacc * 16 * 64 * rw > SPLIT_PART_FLOATS) a.ksw = 1;
+            }
             e = launch_gemm_mf(fmt, epi, a, B, rw, st);
         } else {
             a.ksw = auto_splits(a0, epi, false, 64 * rw, nacc * B * 64 * rw);
