@@ -81,6 +81,31 @@ def pmc_traffic(kclass, batch):
     return None
 
 
+def launch_floor(plane, n=896, iters=200):
+    """Time per launch of a graph-replayed chain of dependent kernels whose workgroups each read
+    the n floats the previous launch wrote (bh_time_probe's chain mode): the floor under every
+    dependent kernel of the decode step, at 14, 36 and 256 workgroups."""
+    from bramha_amd import ops
+
+    out = {}
+    for wgs in (14, 36, 256):
+        out[str(wgs)] = round(ops.time_probe(plane, 2, n * 4, wgs, 4, iters=iters), 3)
+    log("dependent-launch floor (us per launch at 14 / 36 / 256 workgroups): %s" % out)
+    return out
+
+
+def above_floor(roof, floor):
+    """Per kernel class: mean launch time minus the dependent-launch floor, and the step's
+    launch count times that floor (the floor of the 256-workgroup chain, the largest of the
+    three)."""
+    f = max(floor.values())
+    cls = {k: round(v - f, 3) for k, v in roof["per_class_us"].items() if roof["launches_per_step"].get(k)}
+    n = sum(roof["launches_per_step"].values())
+    tot = sum(roof["per_class_us"][k] * c for k, c in roof["launches_per_step"].items())
+    return {"floor_us": f, "chain_us_by_workgroups": floor, "above_floor_us": cls, "launches_per_step": n,
+            "step_kernel_us": round(tot, 1), "step_floor_us": round(n * f, 1), "step_above_floor_us": round(tot - n * f, 1)}
+
+
 def roofline(m, n_steps=16, batch=1):
     """Per-kernel-class mean launch durations over eager decode steps (HIP events on the
     model's stream) and the algorithmic bytes of one launch; the dominant class is the one
@@ -442,6 +467,9 @@ def main():
                     help="only the ragged 32-sequence decode and the Qwen2-7B prefill + decode")
     ap.add_argument("--profile-eager", type=int, default=0, metavar="BATCH",
                     help="for counter collection: only eager (non-graph) decode steps at this batch, kernel by kernel")
+    ap.add_argument("--profile-7b", type=int, default=0, metavar="BATCH",
+                    help="eager decode steps of a 2-layer model at Qwen2-7B widths (with its 152064-row LM "
+                         "head) at this batch, for counter profiles of the 7B kernels")
     ap.add_argument("--profile-prefill", action="store_true",
                     help="for counter collection: only a 2047-token prefill of the Qwen2-7B shape")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
@@ -472,6 +500,24 @@ def main():
         m.close()
         plane.close()
         return
+    if args.profile_7b:
+        from bramha_amd import BH_Q4_G32
+        from bramha_amd.model import QWEN2_7B, DecoderConfig, HipDecoder, synth_tokens, synth_weights
+
+        b = args.profile_7b
+        cfg = DecoderConfig(**dict(QWEN2_7B, n_layers=2), wfmt=BH_Q4_G32, head_fmt=BH_Q4_G32, kv_f16=True,
+                            max_seqs=b, kv_rows=b * 1024, max_tokens=64, tied=False)
+        m = HipDecoder(plane, cfg)
+        m.load(synth_weights(cfg, seed=0))
+        for s_ in range(b):
+            m.seq_open(s_, 1024)
+            m.prefill(s_, synth_tokens(0, "7b.profile.%d" % s_, 8, cfg.vocab))
+        m.decode_setup(list(range(b)), [1] * b)
+        t = m.time_kernels(8)
+        print(json.dumps({k: v[0] for k, v in t.items()}), flush=True)
+        m.close()
+        plane.close()
+        return
     if args.profile_prefill:
         print(json.dumps({"qwen2_7b": qwen7b(plane, steps=0, batches=(1,))}), flush=True)
         plane.close()
@@ -492,17 +538,21 @@ def main():
         plane.close()
         return
     log("building bs1 model")
+    floor = launch_floor(plane)
     m1, cfg = build_model(plane, 1, args.prompt, total + 32)
     dt1 = timed_decode(m1, args.steps, args.warmup)
     tok1 = args.steps / dt1
     log("bs1: %.1f tok/s (%.3f ms/step)" % (tok1, dt1 * 1e3 / args.steps))
     kern, roof = roofline(m1, batch=1)
+    roof["floor"] = above_floor(roof, floor)
     log("dominant kernel %s: %.1f GB/s (%.1f%% of HBM peak)" % (kern, roof["achieved"], 100 * roof["frac"]))
+    log("bs1 time above the dependent-launch floor: %s" % roof["floor"])
     m1.close()
     log("building bs32 model")
     m32, _ = build_model(plane, 32, args.prompt, total + 32)
     dt32 = timed_decode(m32, args.steps, args.warmup)
     kern32, roof32 = roofline(m32, batch=32)
+    roof32["floor"] = above_floor(roof32, floor)
     bs32 = {"value": 32 * args.steps / dt32, "unit": "tok/s", "ms_per_step": dt32 * 1e3 / args.steps,
             "batch": 32, "roofline": roof32}
     log("bs32: %.1f tok/s (%.3f ms/step); dominant kernel %s: %.1f GB/s" %

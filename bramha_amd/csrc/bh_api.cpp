@@ -787,8 +787,8 @@ int bh_time_gemv(bh_ctx* ctx, const bh_weight* wh, const float* x, float* y, int
 }
 
 int bh_time_probe(bh_ctx* ctx, int copy, size_t bytes, int wgs, int unroll, int iters, double* us_per_launch) {
-    if (!ctx || bytes < 16 || wgs <= 0 || wgs > (1 << 20) || iters <= 0 || !us_per_launch ||
-        !(unroll == 4 || unroll == 8 || unroll == 16))
+    if (!ctx || bytes < 16 || wgs <= 0 || wgs > (1 << 20) || iters <= 0 || !us_per_launch || copy < 0 || copy > 2 ||
+        !(unroll == 4 || unroll == 8 || unroll == 16) || (copy == 2 && bytes > (64u << 20)))
         return BH_ERR_INVALID;
     std::lock_guard<std::mutex> g(ctx->mu);
     bytes &= ~(size_t)15;
@@ -799,7 +799,9 @@ int bh_time_probe(bh_ctx* ctx, int copy, size_t bytes, int wgs, int unroll, int 
     if (e == hipSuccess && !copy) e = hipMalloc(&sink, (size_t)wgs * 256 * 4);
     int rc = e == hipSuccess ? BH_OK : ctx->hip_fail(e, "hipMalloc(probe buffers)");
     if (rc == BH_OK)
-        rc = time_graph(ctx, iters, [&](int, hipStream_t st) {
+        rc = time_graph(ctx, iters, [&](int i, hipStream_t st) {
+            if (copy == 2)  // the chain ping-pongs between the two buffers
+                return launch_probe(2, i & 1 ? dst : src, i & 1 ? src : dst, (int64_t)bytes, wgs, unroll, nullptr, st);
             return launch_probe(copy, src, dst, (int64_t)bytes, wgs, unroll, (uint32_t*)sink, st);
         }, us_per_launch);
     if (src) hipFree(src);

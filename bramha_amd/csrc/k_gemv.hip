@@ -201,7 +201,9 @@ static int auto_splits(const GemvArgs& a, int epi, bool mfma, int rows_per_tile,
     // 18944 x 3584 gate/up pair: 25.2 us unsplit, 23.2 at 7 splits, 24.4 at 2, 26.9 at 14) takes
     // 16-chunk splits; not the LM head, whose split would add a reduction to its argmax epilogue.
     if (!(a.C >= 64)) ksw = 1;
-    else if (mfma) ksw = tiles < 256 ? gemv_splits(tiles, a.C, 16, 512) : 1;
+    // (MFMA passes over 256+ row tiles and a long K aim at ~1200 workgroups: the 7B gate/up pair
+    // at 16 tokens 67.7 us unsplit, 57.2 / 52.2 / 50.0 / 55.1 us at 2 / 3 / 4 / 6 splits)
+    else if (mfma) ksw = tiles < 256 ? gemv_splits(tiles, a.C, 16, 512) : (epi == EPI_LMHEAD ? 1 : gemv_splits(tiles, a.C, 16, 1200));
     else if (tiles < 128) ksw = std::min(gemv_splits(tiles, a.C, 16, 256), 8);
     else ksw = (a.batch == 1 && a.C >= 100 && epi != EPI_LMHEAD) ? std::min(a.C / 16, 8) : 1;
     while (ksw > 1 && (int64_t)tiles * ksw * tot > (int64_t)SPLIT_PART_FLOATS) --ksw;

@@ -49,16 +49,30 @@ __global__ void __launch_bounds__(256) k_copy_probe(const u32x4* __restrict__ sr
     }
 }
 
+// One link of a dependent launch chain: every workgroup reads the n floats the previous launch
+// wrote (from another XCD's L2, as a decode kernel reads its producer's activations) and
+// workgroup 0 writes the next n. Nothing else: its graph-replayed time per launch is the floor
+// of a dependent kernel in the decode step.
+__global__ void __launch_bounds__(256) k_chain_probe(const float* __restrict__ src, float* __restrict__ dst, int n) {
+    float v = 0.f;
+    for (int i = threadIdx.x; i < n; i += 256) v += src[i];
+    if (blockIdx.x == 0)
+        for (int i = threadIdx.x; i < n; i += 256) dst[i] = src[i] + (v == 1.0e30f ? 1.f : 0.f);
+}
+
 }  // namespace
 
-// One probe launch: copy = 0 reads src (sink holds wgs * 256 words), copy = 1 copies src to dst.
+// One probe launch: copy = 0 reads src (sink holds wgs * 256 words), copy = 1 copies src to dst,
+// copy = 2 is one link of the dependent chain (bytes / 4 floats from src to dst).
 hipError_t launch_probe(int copy, const void* src, void* dst, int64_t bytes, int wgs, int unroll, uint32_t* sink,
                         hipStream_t st) {
     const int64_t n16 = bytes / 16;
     if (n16 <= 0 || wgs <= 0 || (copy && !dst) || (!copy && !sink)) return hipErrorInvalidValue;
     const dim3 g((unsigned)wgs), b(256);
     const u32x4* s = (const u32x4*)src;
-    if (copy) {
+    if (copy == 2) {
+        launch_kernel(k_chain_probe, g, b, 0, st, (const float*)src, (float*)dst, (int)(bytes / 4));
+    } else if (copy) {
         switch (unroll) {
             case 4: launch_kernel(k_copy_probe<4>, g, b, 0, st, s, (u32x4*)dst, n16); break;
             case 8: launch_kernel(k_copy_probe<8>, g, b, 0, st, s, (u32x4*)dst, n16); break;

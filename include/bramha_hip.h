@@ -180,7 +180,10 @@ int bh_time_attn(bh_ctx* ctx, const float* q, const void* k, const void* v, int 
  * the 256 MB Infinity Cache, so every launch reads HBM) with 16-byte non-temporal loads (copy = 0),
  * or copy it into a second buffer (copy = 1); wgs workgroups of 256 threads, `unroll` (4, 8 or 16)
  * loads in flight per thread. Returns the mean microseconds per launch; the achievable read (copy)
- * bandwidth is bytes (2 * bytes) / time. The buffers are allocated and freed by the call. */
+ * bandwidth is bytes (2 * bytes) / time. copy = 2 times a chain of dependent launches instead:
+ * each of its wgs workgroups reads the bytes / 4 floats the previous launch wrote (workgroup 0
+ * writes the next), replayed as a graph like the decode step, so the time per launch is the floor
+ * of one dependent decode kernel. The buffers are allocated and freed by the call. */
 int bh_time_probe(bh_ctx* ctx, int copy, size_t bytes, int wgs, int unroll, int iters, double* us_per_launch);
 
 /* ------------------------------------------------------------ decoder model */
