@@ -148,10 +148,22 @@ int upload_rows(bh_ctx* ctx, DevWeight& dst, int64_t row0, int64_t n, const void
     const int64_t np_src = pad64(n);
     hipError_t e = hipMemcpy2D((uint8_t*)dst.q + row0 * 16, (size_t)dst.n_pad * 16, hq, (size_t)np_src * 16,
                                (size_t)n * 16, (size_t)dst.chunks, hipMemcpyHostToDevice);
-    if (e == hipSuccess && dst.fmt == BH_Q4_G32)
-        e = hipMemcpy2D((uint8_t*)dst.s + row0 * 2, (size_t)dst.n_pad * 2, hs, (size_t)np_src * 2, (size_t)n * 2,
-                        (size_t)dst.chunks, hipMemcpyHostToDevice);
-    else if (e == hipSuccess && (dst.fmt == BH_Q8_ROW || dst.fmt == BH_Q4_ROW))
+    if (e == hipSuccess && dst.fmt == BH_Q4_G32) {
+        // group scales: staged [C][n] on the device, then scattered to their sc_pos places (a row
+        // range need not start on a 64-row group, and the other rows of its groups may already hold
+        // another upload's scales)
+        void* tmp = nullptr;
+        e = hipMalloc(&tmp, (size_t)n * 2 * (size_t)dst.chunks);
+        if (e == hipSuccess)
+            e = hipMemcpy2D(tmp, (size_t)n * 2, hs, (size_t)np_src * 2, (size_t)n * 2, (size_t)dst.chunks,
+                            hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = launch_scatter_scales(dst.s, tmp, row0, n, dst.n_pad, dst.chunks, nullptr);
+        if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+        if (tmp) {
+            const hipError_t f = hipFree(tmp);
+            if (e == hipSuccess) e = f;
+        }
+    } else if (e == hipSuccess && (dst.fmt == BH_Q8_ROW || dst.fmt == BH_Q4_ROW))
         e = hipMemcpy((float*)dst.s + row0, hs, (size_t)n * 4, hipMemcpyHostToDevice);
     free(hq);
     free(hs);

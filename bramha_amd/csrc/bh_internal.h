@@ -20,10 +20,20 @@ namespace bh {
 // contiguous weights per chunk step while the activations for that chunk are
 // the same for every lane (scalar loads). Q4 chunks keep the reference's byte
 // order: byte b of the chunk holds elements 2b (high nibble) and 2b+1 (low).
-// Scales: BH_Q4_G32 fp16 [C][n_pad] (chunk c == group c), row formats f32 [n_pad].
+// Scales: BH_Q4_G32 fp16 [C][n_pad] (chunk c == group c) with the rows of every 64-row group
+// permuted (sc_pos), row formats f32 [n_pad].
 // ---------------------------------------------------------------------------
 inline int chunk_elems(int fmt) { return fmt == BH_Q4_ROW || fmt == BH_Q4_G32 ? 32 : (fmt == BH_Q8_ROW ? 16 : 4); }
 inline int64_t pad64(int64_t n) { return (n + 63) / 64 * 64; }
+
+// Position of row r's fp16 group scale in its chunk's run of n_pad: within a 64-row group, row
+// 16 rb + 4 g + v (rb, g, v < 4) sits at 16 g + 4 rb + v. An MFMA wavefront's lanes of group g
+// hold D rows 4 g .. 4 g + 3 of each 16-row block rb, so their scales for all four blocks are
+// 32 contiguous bytes (two 16-byte loads instead of four 8-byte ones); a lane that owns one row
+// (the VALU GEMV) reads its scale at sc_pos(row) as before at row.
+__host__ __device__ constexpr inline int64_t sc_pos(int64_t r) {
+    return (r & ~(int64_t)63) | (((r >> 2) & 3) << 4) | (((r >> 4) & 3) << 2) | (r & 3);
+}
 
 struct DevWeight {
     int fmt = BH_F32;
@@ -209,6 +219,9 @@ hipError_t launch_rmsnorm(const float* x, const float* w, float eps, float* out,
 hipError_t launch_rope(float* v, const int32_t* pos, const float2* tab, int rows, int n_heads, int hd, hipStream_t st);
 hipError_t launch_silu_mul(const float* g, const float* u, float* out, int64_t n, hipStream_t st);
 hipError_t launch_dequant(const DevWeight& w, float* out, hipStream_t st);
+// Group-32 scales of rows [row0, row0 + n), src [C][n] in device memory, to their sc_pos places.
+hipError_t launch_scatter_scales(void* dst, const void* src, int64_t row0, int64_t n, int64_t n_pad, int64_t C,
+                                 hipStream_t st);
 // Rows [row0, row0 + n) (absolute rows of the packed buffer) of one layer's cache <-> f32
 // [n][nkv][hd] (to_host = 1: cache -> kh / vh; 0: kh / vh -> cache).
 hipError_t launch_kv_copy(const KvView& kv, int nkv, int hd, int64_t row0, int64_t n, float* kh, float* vh, int to_host,

@@ -103,7 +103,7 @@ __global__ void __launch_bounds__(64 * AO_WAVES) k_attn_o(const AttnArgs at, con
         for (int u = 0; u < U; ++u) {
             const int cc = max(min(c0 + u, c1 - 1), 0);
             wq[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rW, (int)nl * 16, cc * a.n_pad * 16, 0));
-            ws[u] = __builtin_amdgcn_raw_buffer_load_b16(rS, (int)nl * 2, cc * a.n_pad * 2, 0);
+            ws[u] = __builtin_amdgcn_raw_buffer_load_b16(rS, (int)sc_pos(nl) * 2, cc * a.n_pad * 2, 0);
         }
     };
     EpiPre<EPI_RESNORM> pre;

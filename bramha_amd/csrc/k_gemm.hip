@@ -9,7 +9,8 @@
 // fixed order) and, for matrices with few row tiles, over workgroups (the ordered split
 // reduction of k_epilogue.h).
 // Each wavefront runs v_mfma_f32_16x16x32_f16 over its 64 rows as four 16-row A blocks — one
-// dword of 8 nibbles per lane per block, decoded to exact fp16 (q - 8) — with the tokens as the
+// 16-byte load of a row's chunk per lane, transposed across the lane groups into one dword of
+// 8 nibbles per lane per block (rows_to_a), decoded to exact fp16 (q - 8) — with the tokens as the
 // B operand: f32 activations split into fp16 hi + lo (hi + lo carries ~22 bits), so each product
 // takes two MFMAs and the B operand of a chunk is shared by the four row blocks. All loads are
 // raw buffer loads (SGPR resource, per-lane VGPR offset, per-chunk SGPR offset) issued
@@ -27,8 +28,8 @@ namespace {
 
 template <int NACC, int TB, int S>
 struct MfStage {
-    uint32_t w[S][NACC][4];  // [chunk][matrix][row block]: dword lg of row rb * 16 + lr
-    uint2 s[S][NACC][4];     // fp16 group scales of rows rb * 16 + 4 lg .. + 3
+    uint32_t w[S][NACC][4];  // [chunk][matrix]: the chunk of row n0 + lane (rows_to_a makes it A operands)
+    uint4 s[S][NACC][2];     // fp16 group scales of rows rb * 16 + 4 lg .. + 3, rb = 0 .. 3 (sc_pos order)
     uint4 x[S][TB][2];       // f32 activations of token tb * 16 + lr, k = 8 lg .. + 7
 };
 
@@ -83,15 +84,21 @@ __global__ void __launch_bounds__(64 * KW * RW) k_gemm_mf(const GemvArgs a0) {
         for (int u = 0; u < S; ++u) {
             const int cc = min(c + u, c1 - 1);
 #pragma unroll
-            for (int j = 0; j < NACC; ++j)
+            for (int j = 0; j < NACC; ++j) {
+                const uint4 q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rW[j], (n0 + lane) * 16,
+                                                                                               cc * a.n_pad * 16, 0));
+                st.w[u][j][0] = q.x;
+                st.w[u][j][1] = q.y;
+                st.w[u][j][2] = q.z;
+                st.w[u][j][3] = q.w;
+                if constexpr (FMT == BH_Q4_G32) {
+                    // n0 is a multiple of 64: sc_pos puts this lane group's 16 rows at n0 + 16 lg
 #pragma unroll
-                for (int rb = 0; rb < 4; ++rb) {
-                    st.w[u][j][rb] = __builtin_amdgcn_raw_buffer_load_b32(rW[j], (n0 + rb * 16 + lr) * 16 + 4 * lg,
-                                                                           cc * a.n_pad * 16, 0);
-                    if constexpr (FMT == BH_Q4_G32)
-                        st.s[u][j][rb] = __builtin_bit_cast(
-                            uint2, __builtin_amdgcn_raw_buffer_load_b64(rS[j], (n0 + rb * 16 + 4 * lg) * 2, cc * a.n_pad * 2, 0));
+                    for (int h = 0; h < 2; ++h)
+                        st.s[u][j][h] = __builtin_bit_cast(
+                            uint4, __builtin_amdgcn_raw_buffer_load_b128(rS[j], (n0 + 16 * lg) * 2 + 16 * h, cc * a.n_pad * 2, 0));
                 }
+            }
 #pragma unroll
             for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
@@ -109,6 +116,7 @@ __global__ void __launch_bounds__(64 * KW * RW) k_gemm_mf(const GemvArgs a0) {
 #pragma unroll
             for (int tb = 0; tb < TB; ++tb) acc[j][rb][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+    const Dec8K mg = dec8_consts();
     auto consume = [&](int c, const MfStage<NACC, TB, S>& st) {
 #pragma unroll
         for (int u = 0; u < S; ++u) {
@@ -119,12 +127,14 @@ __global__ void __launch_bounds__(64 * KW * RW) k_gemm_mf(const GemvArgs a0) {
                     split8(__builtin_bit_cast(float4, st.x[u][tb][0]), __builtin_bit_cast(float4, st.x[u][tb][1]), bh[tb],
                            bl[tb]);
 #pragma unroll
-                for (int j = 0; j < NACC; ++j)
+                for (int j = 0; j < NACC; ++j) {
+                    uint32_t wa[4] = {st.w[u][j][0], st.w[u][j][1], st.w[u][j][2], st.w[u][j][3]};
+                    rows_to_a(wa);
 #pragma unroll
                     for (int rb = 0; rb < 4; ++rb) {
-                        const half8 av = dec8(st.w[u][j][rb]);
+                        const half8 av = dec8(wa[rb], mg);
                         if constexpr (FMT == BH_Q4_G32) {
-                            const __half2* s2 = (const __half2*)&st.s[u][j][rb];
+                            const __half2* s2 = (const __half2*)&st.s[u][j][0] + 2 * rb;
                             const float2 sa = __half22float2(s2[0]), sb = __half22float2(s2[1]);
 #pragma unroll
                             for (int tb = 0; tb < TB; ++tb) {
@@ -143,6 +153,7 @@ __global__ void __launch_bounds__(64 * KW * RW) k_gemm_mf(const GemvArgs a0) {
                             }
                         }
                     }
+                }
             }
         }
     };

@@ -50,7 +50,7 @@ __device__ __forceinline__ void lh_unkey(unsigned long long k, float& v, int& id
 
 struct LhStage {
     uint32_t w[LH_RBMAX];  // dword lg of row rb * 16 + lr
-    uint2 s[LH_RBMAX];     // fp16 group scales of rows rb * 16 + 4 lg .. + 3
+    uint2 s[LH_RBMAX];     // fp16 group scales of rows rb * 16 + 4 lg .. + 3 (contiguous at sc_pos)
 };
 
 struct LhCtx {
@@ -68,7 +68,7 @@ __device__ __forceinline__ void lh_fetch(const LhCtx& k, int n0, int c, LhStage&
         const int nb = min(n0 + rb * 16, k.n_pad - 16);
         st.w[rb] = __builtin_amdgcn_raw_buffer_load_b32(k.rW, (nb + k.lr) * 16 + 4 * k.lg, c * k.n_pad * 16, CPOL_STREAM);
         st.s[rb] = __builtin_bit_cast(
-            uint2, __builtin_amdgcn_raw_buffer_load_b64(k.rS, (nb + 4 * k.lg) * 2, c * k.n_pad * 2, CPOL_STREAM));
+            uint2, __builtin_amdgcn_raw_buffer_load_b64(k.rS, (int)sc_pos(nb + 4 * k.lg) * 2, c * k.n_pad * 2, CPOL_STREAM));
     }
 }
 

@@ -58,6 +58,23 @@ __device__ __forceinline__ half8 dec8(uint32_t w, const Dec8K& k) {
     return r;
 }
 
+// A operands of a 64-row group from one 16-byte load per lane: on entry d[g] is dword g of the
+// chunk of row `lane` (lane l loaded row n0 + l); on exit d[rb] is dword lg of row rb * 16 + lr,
+// the A operand of row block rb. A 4 x 4 transpose across the four 16-lane groups: lanes swap
+// with the lane 32 away, then with the lane 16 away (v_permlane32_swap, v_permlane16_swap).
+// One load instead of four per chunk: the four dword loads of every chunk were what the
+// memory pipeline of a CU queued most of.
+__device__ __forceinline__ void rows_to_a(uint32_t (&d)[4]) {
+    const auto p0 = __builtin_amdgcn_permlane32_swap(d[0], d[2], false, false);
+    const auto p1 = __builtin_amdgcn_permlane32_swap(d[1], d[3], false, false);
+    const auto q0 = __builtin_amdgcn_permlane16_swap(p0[0], p1[0], false, false);
+    const auto q1 = __builtin_amdgcn_permlane16_swap(p0[1], p1[1], false, false);
+    d[0] = q0[0];
+    d[1] = q0[1];
+    d[2] = q1[0];
+    d[3] = q1[1];
+}
+
 // f32 activations -> fp16 hi + lo (hi + lo carries ~22 bits of the f32 mantissa).
 __device__ __forceinline__ void split8(const float4& x0, const float4& x1, half8& hi, half8& lo) {
     const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};

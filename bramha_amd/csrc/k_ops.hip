@@ -68,7 +68,7 @@ __global__ void k_dequant(int fmt, const uint4* __restrict__ Q, const void* __re
     const uint32_t w[4] = {q.x, q.y, q.z, q.w};
     float* o = out + row * k;
     if (fmt == BH_Q4_ROW || fmt == BH_Q4_G32) {
-        const float sc = fmt == BH_Q4_G32 ? __half2float(((const __half*)S)[c * n_pad + row]) : ((const float*)S)[row];
+        const float sc = fmt == BH_Q4_G32 ? __half2float(((const __half*)S)[c * n_pad + sc_pos(row)]) : ((const float*)S)[row];
         for (int j = 0; j < 16; ++j) {
             const uint32_t byte = (w[j >> 2] >> (8 * (j & 3))) & 0xFFu;
             o[c * 32 + 2 * j] = ((float)((byte >> 4) & 0x0F) - 8.0f) * sc;
@@ -93,7 +93,7 @@ __device__ __forceinline__ float embed_elem(const DevWeight& t, int64_t id, int 
     if (t.fmt == BH_F32) return ((const float*)t.q)[(c * t.n_pad + id) * 4 + (i & 3)];
     const uint8_t byte = ((const uint8_t*)t.q)[(c * t.n_pad + id) * 16 + ((i & 31) >> 1)];
     const float nib = (i & 1) ? (float)(byte & 0x0F) : (float)((byte >> 4) & 0x0F);
-    return (nib - 8.0f) * __half2float(((const __half*)t.s)[c * t.n_pad + id]);
+    return (nib - 8.0f) * __half2float(((const __half*)t.s)[c * t.n_pad + sc_pos(id)]);
 }
 
 // Residual stream of token row b from embedding row `id`: x, xw = x * w0, and per-64-element
@@ -395,6 +395,25 @@ hipError_t launch_kv_copy(const KvView& kv, int nkv, int hd, int64_t row0, int64
     if (total <= 0) return hipSuccess;
     const int64_t blocks = std::min<int64_t>((total + 255) / 256, 16384);
     launch_kernel(k_kv_copy, dim3((unsigned)blocks), dim3(256), 0, st, kv, nkv, hd, row0, n, kh, vh, to_host);
+    return hipGetLastError();
+}
+
+// Rows [row0, row0 + n) of a group-32 scale matrix from src ([C][n], the reference's row order)
+// into dst ([C][n_pad], rows at sc_pos): one thread per scale.
+__global__ void k_scatter_scales(uint16_t* __restrict__ dst, const uint16_t* __restrict__ src, int64_t row0, int64_t n,
+                                 int64_t n_pad, int64_t C) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n * C) return;
+    const int64_t c = t / n, i = t % n;
+    dst[c * n_pad + sc_pos(row0 + i)] = src[t];
+}
+
+hipError_t launch_scatter_scales(void* dst, const void* src, int64_t row0, int64_t n, int64_t n_pad, int64_t C,
+                                 hipStream_t st) {
+    const int64_t total = n * C;
+    if (total <= 0) return hipSuccess;
+    launch_kernel(k_scatter_scales, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, (uint16_t*)dst,
+                  (const uint16_t*)src, row0, n, n_pad, C);
     return hipGetLastError();
 }
 

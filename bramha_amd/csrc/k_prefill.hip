@@ -106,7 +106,7 @@ __global__ void __launch_bounds__(256) k_gemm_pf(const GemvArgs a) {
                                                                    cc * a.n_pad * 16, 0);
                 if constexpr (FMT == BH_Q4_G32)
                     st.s[j][rb] = __builtin_bit_cast(
-                        uint2, __builtin_amdgcn_raw_buffer_load_b64(rS[j], (n0 + rb * 16 + 4 * lg) * 2, cc * a.n_pad * 2, 0));
+                        uint2, __builtin_amdgcn_raw_buffer_load_b64(rS[j], (int)sc_pos(n0 + rb * 16 + 4 * lg) * 2, cc * a.n_pad * 2, 0));
             }
 #pragma unroll
         for (int tb = 0; tb < TBW; ++tb)
@@ -268,7 +268,7 @@ __global__ void __launch_bounds__(256, 2) k_gemm_pfl(const GemvArgs a) {
             r.b[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rX, vo_b[k], cc * 128, 0));
         if (aload) {
             r.w = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rW, grow * 16, cc * a.n_pad * 16, 0));
-            if constexpr (FMT == BH_Q4_G32) r.s = __builtin_amdgcn_raw_buffer_load_b16(rS, grow * 2, cc * a.n_pad * 2, 0);
+            if constexpr (FMT == BH_Q4_G32) r.s = __builtin_amdgcn_raw_buffer_load_b16(rS, (int)sc_pos(grow) * 2, cc * a.n_pad * 2, 0);
         }
     };
     auto store = [&](const Regs& r, int stage) {

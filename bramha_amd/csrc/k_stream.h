@@ -88,7 +88,7 @@ __device__ __forceinline__ void stream_chunks(const GemvArgs& a, int64_t nl, int
         rW[1] = __builtin_amdgcn_make_buffer_rsrc((void*)a.W2, (short)0, a.C * a.n_pad * 16, 0x00020000);
         rS[1] = __builtin_amdgcn_make_buffer_rsrc((void*)a.S2, (short)0, a.C * a.n_pad * 2, 0x00020000);
     }
-    const int vo_w = (int)nl * 16, vo_s = (int)nl * 2;
+    const int vo_w = (int)nl * 16, vo_s = (int)sc_pos(nl) * 2;
     uint4 q0[NACC][U], q1[NACC][U];
     // scales as raw fp16 bits, each in its own 32-bit register (packing two per register would
     // make the first stage wait on its scale loads before mid() issues anything)

@@ -81,6 +81,20 @@ def test_gemv_q4g32_qwen_shapes(plane, n, k, batch):
 
 
 @pytest.mark.parametrize("fmt", [BH_Q4_G32, BH_Q4_ROW])
+@pytest.mark.parametrize("n,k", [(37, 96), (300, 96), (1000, 896)])
+@pytest.mark.parametrize("batch", [1, 9, 16, 32, 40, 63])
+def test_gemv_ragged_rows(plane, fmt, n, k, batch):
+    """Row counts that end inside a 64-row group (the padded rows and the group-32 scales of a
+    partial group) through the VALU GEMV (batch 1), the MFMA passes (9..32 tokens) and the
+    16-token-group passes (33..63)."""
+    w = _w(fmt * 13 + n + k, n, k)
+    q, s, deq = _quant(fmt, w)
+    x = np.random.default_rng(n + batch).standard_normal((batch, k)).astype(np.float32)
+    y = ops.DeviceWeight(plane, fmt, n, k, q, s).gemv(ops.DeviceArray.from_numpy(plane, x)).numpy()
+    _check_gemv(y, deq, x)
+
+
+@pytest.mark.parametrize("fmt", [BH_Q4_G32, BH_Q4_ROW])
 @pytest.mark.parametrize("n,k,batch", [(896, 896, 64), (896, 896, 257), (4864, 896, 130), (896, 4864, 200), (300, 96, 71)])
 def test_gemv_prefill_tiles(plane, fmt, n, k, batch):
     """Token counts of prefill chunks (>= 64): one tiled MFMA launch over all tokens, with ragged
