@@ -307,7 +307,7 @@ __device__ __forceinline__ void run_resnorm_pre(const GemvArgs& a, const float* 
 #pragma unroll
     for (int k = 0; k < ResPre<B, ROWS, NT>::PER; ++k) {
         const int i = threadIdx.x + k * NT;
-        if (i >= B * ROWS) continue;
+        if (i >= B * ROWS) continue;  // uniform over the wavefront
         const int b = i / ROWS;
         const int64_t nn = row0 + i % ROWS;
         float sq = 0.f;
@@ -329,17 +329,13 @@ __device__ __forceinline__ void run_resnorm_pre(const GemvArgs& a, const float* 
             }
             sq = v * v;
         }
-        scratch[i] = sq;
+        // the wavefront's 64 elements are rows 64 sub .. + 63 of token b (NT and ROWS are multiples
+        // of 64), lane = row: the tile's sum of squares in the order of the other epilogues
+        const float t = wave_sum64(sq);
+        const int64_t tile = (row0 + i % ROWS) / 64;
+        if ((threadIdx.x & 63) == 0 && b < a.batch && tile < a.ssq_tiles) a.ssq_out[(int64_t)b * a.ssq_tiles + tile] = t;
     }
-    lds_barrier();  // LDS scratch only: the stores above need not complete
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    constexpr int SUB = ROWS / 64;
-    for (int q = wave; q < B * SUB; q += NT / 64) {
-        const int b = q / SUB, sub = q % SUB;
-        const float t = wave_sum64(scratch[b * ROWS + sub * 64 + lane]);
-        const int64_t tile = row0 / 64 + sub;
-        if (lane == 0 && b < a.batch && tile < a.ssq_tiles) a.ssq_out[(int64_t)b * a.ssq_tiles + tile] = t;
-    }
+    (void)scratch;
 }
 
 // The batched LM-head epilogue with the counts of PenPre (run_epilogue's EPI_LMHEAD otherwise).

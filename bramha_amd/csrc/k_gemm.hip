@@ -36,7 +36,7 @@ struct MfStage {
 // blockIdx.y: token group, tokens blockIdx.y * B .. + B - 1 of the launch's arguments (a pass
 // of 32 tokens can run as two groups of 16: twice the workgroups, nothing shared between them),
 // each group with its own region of the split scratch.
-template <int FMT, int B, int EPI, int RW, int KW, int S>
+template <int FMT, int B, int EPI, int RW, int KW, int S, bool ONE_ROUND>
 __global__ void __launch_bounds__(64 * KW * RW) k_gemm_mf(const GemvArgs a0) {
     constexpr int NACC = EPI == EPI_SILU ? 2 : 1;
     constexpr int ROWS = 64 * RW;
@@ -51,7 +51,7 @@ __global__ void __launch_bounds__(64 * KW * RW) k_gemm_mf(const GemvArgs a0) {
     extern __shared__ float smem[];
     float* rn = smem;          // [32] per-token norm factors
     float* comb = smem + 32;   // [NACC][B][ROWS] sums, then epilogue scratch [B][ROWS]
-    float* tree = comb + TOT;  // [KW / 2][B][ROWS + 4] wave-sum exchange (before the epilogue)
+    float* tree = comb + TOT;  // [KW or KW / 2][B][ROWS + 4] wave-sum exchange (before the epilogue)
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -181,18 +181,43 @@ __global__ void __launch_bounds__(64 * KW * RW) k_gemm_mf(const GemvArgs a0) {
     }
 
     rq.finish(a, rn);  // read by the epilogue, after the barriers below
-    // D layout: lane holds token tb * 16 + lr, rows 4 * lg + v of each 16-row block. The K-split
-    // waves of a row group halve in rounds: waves [h, 2h) hand their sums to waves [0, h) through
-    // LDS; wave 0 ends with the group's total. In the exchange buffers a token's rows are TS =
-    // ROWS + 4 floats apart and row 4 lg + v of a block sits at 4 v + lg, so the 64 lanes of one
-    // D element fall in 64 distinct banks (4 lr + lg); with rows in natural order at stride ROWS
-    // the 16 lr lanes shared a bank (16-way conflicts: 94K conflict cycles of 420K busy on
-    // 896 x 896 at 32 tokens). The totals are copied to comb's [j][b][row] order at the end.
+    // D layout: lane holds token tb * 16 + lr, rows 4 * lg + v of each 16-row block. In the
+    // exchange buffers a token's rows are TS = ROWS + 4 floats apart and row 4 lg + v of a block
+    // sits at 4 v + lg, so the 64 lanes of one D element fall in 64 distinct banks (4 lr + lg);
+    // with rows in natural order at stride ROWS the 16 lr lanes shared a bank (16-way conflicts:
+    // 94K conflict cycles of 420K busy on 896 x 896 at 32 tokens).
     constexpr float FIN = FMT == BH_Q4_ROW ? 16.0f : 1.0f;  // row formats: the epilogue scales by s/16
     constexpr int TS = ROWS + 4;
     auto at = [&](int rb, int tb, int v) { return (tb * 16 + lr) * TS + rw * 64 + rb * 16 + 4 * v + lg; };
+    if constexpr (ONE_ROUND) {
+        // every K-split wave stores its sums in its own buffer, one barrier, then each thread adds
+        // the KW partials of its comb elements in wave order (2 barriers per matrix instead of
+        // the 2 log2(KW) + 2 of the halving tree)
+#pragma unroll
+        for (int j = 0; j < NACC; ++j) {
+            float* buf = tree + kw * B * TS;
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) buf[at(rb, tb, v)] = acc[j][rb][tb][v];
+            lds_barrier();
+            // to [b][row]: row r of a 16-row block is at (r & 3) * 4 + (r >> 2) & 3
+            for (int i = threadIdx.x; i < B * ROWS; i += blockDim.x) {
+                const int b = i / ROWS, r = i % ROWS;
+                const float* p = tree + b * TS + (r & ~15) + ((r & 3) << 2) + ((r >> 2) & 3);
+                float t = p[0];
+#pragma unroll
+                for (int w = 1; w < KW; ++w) t += p[w * B * TS];
+                comb[j * B * ROWS + i] = t * FIN;
+            }
+            lds_barrier();
+        }
+    } else
 #pragma unroll
     for (int j = 0; j < NACC; ++j) {
+        // waves [h, 2h) hand their sums to waves [0, h); wave 0 ends with the group's total
 #pragma unroll
         for (int h = KW / 2; h >= 1; h >>= 1) {
             if (kw >= h && kw < 2 * h) {
@@ -250,7 +275,10 @@ hipError_t launch_k(const GemvArgs& a, int groups, hipStream_t st) {
     constexpr int NACC = EPI == EPI_SILU ? 2 : 1;
     constexpr int ROWS = 64 * RW;
     const int tiles = (a.n_pad + ROWS - 1) / ROWS;
-    const size_t shm = (32 + (size_t)NACC * B * ROWS + (size_t)std::max(1, KW / 2) * B * (ROWS + 4)) * sizeof(float);
+    // the one-round wave-sum exchange where its KW buffers fit 64 KiB, else the halving tree
+    const size_t base = (32 + (size_t)NACC * B * ROWS) * sizeof(float);
+    constexpr bool ONE = (32 + (size_t)NACC * B * ROWS + (size_t)KW * B * (ROWS + 4)) * sizeof(float) <= 64 * 1024;
+    const size_t shm = base + (size_t)(ONE ? KW : std::max(1, KW / 2)) * B * (ROWS + 4) * sizeof(float);
     if (shm > 64 * 1024) return hipErrorInvalidValue;
     // 8-wave launches without a K split over workgroups take two chunks per stage (all of a
     // 3.5-chunk wave's loads in flight at once: 896-wide K at 32 tokens, QKV 10.4 -> 10.0 us, O
@@ -258,9 +286,9 @@ hipError_t launch_k(const GemvArgs& a, int groups, hipStream_t st) {
     // (not the 32-token gate/up pair, whose two-chunk stages do not fit the registers)
     constexpr bool S2 = KW == 8 && !(NACC == 2 && B == 32);
     if (S2 && a.ksw == 1)
-        launch_kernel((k_gemm_mf<FMT, B, EPI, RW, KW, S2 ? 2 : 1>), dim3(tiles * a.ksw, groups), dim3(64 * KW * RW), shm, st, a);
+        launch_kernel((k_gemm_mf<FMT, B, EPI, RW, KW, S2 ? 2 : 1, ONE>), dim3(tiles * a.ksw, groups), dim3(64 * KW * RW), shm, st, a);
     else
-        launch_kernel((k_gemm_mf<FMT, B, EPI, RW, KW, 1>), dim3(tiles * a.ksw, groups), dim3(64 * KW * RW), shm, st, a);
+        launch_kernel((k_gemm_mf<FMT, B, EPI, RW, KW, 1, ONE>), dim3(tiles * a.ksw, groups), dim3(64 * KW * RW), shm, st, a);
     return hipGetLastError();
 }
 
