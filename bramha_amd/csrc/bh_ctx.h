@@ -51,6 +51,9 @@ struct bh_ctx {
     // counters, zero when idle); calls on other streams run unsplit so they never share it.
     float* split_part = nullptr;
     int32_t* split_cnt = nullptr;
+    // Limb records of a batch-1 activation row (XL_TMP_CHUNKS chunks) for the GEMVs launched on
+    // the context's own stream, under the same rule.
+    uint32_t* xl_tmp = nullptr;
 
     // Fault injection (bh_debug_inject_fault).
     int inj_op = 0, inj_status = 0, inj_count = 0;

@@ -153,6 +153,14 @@ struct GemvArgs {
     // LM head (k_lmhead.hip) takes its activations from x_hl when set instead of splitting x.
     uint16_t* xw_hl = nullptr;
     const uint16_t* x_hl = nullptr;
+    // Batch-1 activations as int4 limb records (k_xl.h: 32 words per 32-element chunk). xl: the
+    // records of x, written by its producer; a batch-1 Q4_G32 VALU pass then reads them instead
+    // of x. xl_out: a batch-1 EPI_RESNORM / EPI_SILU pass also writes the records of what it
+    // stores (xw_out / y). xl_tmp: room for C records where a caller has only x (the single-op
+    // entry points): the launcher converts x there first.
+    const uint32_t* xl = nullptr;
+    uint32_t* xl_out = nullptr;
+    uint32_t* xl_tmp = nullptr;
 };
 
 // The arguments of tokens b0 .. b0 + n - 1 of `a`: every per-token pointer advanced by b0.
@@ -193,6 +201,10 @@ inline void launch_kernel(K kernel, dim3 grid, dim3 block, size_t shm, hipStream
 
 // Launchers (k_gemv.hip). Return hipSuccess or the launch error.
 hipError_t launch_gemv(int fmt, int epi, const GemvArgs& a, hipStream_t st);
+// Limb records (k_xl.h) of the n floats of x (n rounded up to whole 32-element chunks with zeros).
+hipError_t launch_xl_pack(const float* x, int n, uint32_t* rec, hipStream_t st);
+constexpr int XL_TMP_CHUNKS = 4096;  // chunks of the single-op entry points' record scratch
+constexpr int XL_REC_BYTES = 128;    // bytes of one chunk's limb record (plus 4 of its factor)
 // MFMA GEMM pass of B = 16 or 32 tokens over 4-bit weights (k_gemm.hip), rw * 64 rows per tile.
 hipError_t launch_gemm_mf(int fmt, int epi, const GemvArgs& a, int B, int rw, hipStream_t st);
 // MFMA GEMM over all a.batch tokens at once for prefill chunks (k_prefill.hip): 128-row by
@@ -229,7 +241,7 @@ hipError_t launch_kv_copy(const KvView& kv, int nkv, int hd, int64_t row0, int64
 // Start of the residual stream for `batch` tokens tok[b] % vocab: x = embedding row of the tied
 // table (KM16, F32 or Q4_G32), xw = x * w0, ssq per 64 elements. reset_step != null: zero it.
 hipError_t launch_embed(const DevWeight& table, const int32_t* tok, const float* w0, float* x, float* xw, float* ssq,
-                        int ssq_tiles, int32_t* reset_step, int batch, hipStream_t st);
+                        int ssq_tiles, int32_t* reset_step, int batch, hipStream_t st, uint32_t* xl = nullptr);
 // End of a decode step, one workgroup per batch entry: first-max argmax over the LM head's
 // per-64-row partials; bumps the penalty count of the chosen id; records it at
 // ids_cap[step[b] * batch + b] (ids_cap may be null) and advances step[b]; sets tok[b] to it and
@@ -265,6 +277,7 @@ struct SampleArgs {
     const float* w0 = nullptr;
     float *x = nullptr, *xw = nullptr, *ssq = nullptr;
     int ssq_tiles = 0;
+    uint32_t* xl = nullptr;  // limb records of entry 0's next xw (k_xl.h), for a batch-1 step
 };
 hipError_t launch_sample(const SampleArgs& a, hipStream_t st);
 

@@ -69,6 +69,9 @@ struct bh_model {
     float* split_part = nullptr;   // K-split sums of split projections
     uint16_t* xhl = nullptr;       // prefill passes: activations split into fp16 hi + lo
     uint16_t* xw_hl = nullptr;     // decode: final-norm activations split for the batched LM head
+    // Batch-1 passes: limb records (k_xl.h) of xw, written by every producer of the residual
+    // stream, and of the SwiGLU product mm, written by gate/up; read by the group-32 GEMVs.
+    uint32_t *xl_h = nullptr, *xl_f = nullptr;
     int32_t* split_cnt = nullptr;  // their per-tile arrival counters (zero when idle)
     // decode batch state (read by the captured graph) and prefill staging, kept apart so a
     // prefill between decode calls leaves the batch intact
@@ -204,10 +207,17 @@ static bool lm_presplit(const bh_model* m, int M) {
 // One forward pass over M tokens whose residual stream (x, xw, ssq) holds their embedding rows:
 // the decode batch (decode = true: logits, penalty, argmax and the next step's stream) or a
 // staged prefill chunk.
+// Whether a pass over M tokens carries limb records (k_xl.h) from the producers to the batch-1
+// group-32 GEMVs; the stream's start (launch_embed, k_sample) writes them under the same rule.
+static bool use_xl(const bh_model* m, int M) {
+    return M == 1 && (m->c.wfmt == BH_Q4_G32 || m->c.head_fmt == BH_Q4_G32);
+}
+
 hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) {
     const bh_model_config& c = m->c;
     const int H = c.hidden, I = c.ffn;
     hipStream_t st = m->st;
+    const bool xl = use_xl(m, M);
     int32_t* pos = decode ? m->d_pos : m->d_ppos;
     int32_t* slot = decode ? m->d_slot : m->d_pslot;
     int64_t* boff = decode ? m->d_boff : m->d_pboff;
@@ -228,6 +238,7 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
         a.boff = boff;
         a.rope = m->rope;
         a.kv = kv_view(m, l);
+        if (xl) a.xl = m->xl_h;
         e = timed(m, BH_K_GEMV_QKV, [&] { return launch_gemv(c.wfmt, EPI_QKV, a, st); });
         if (e != hipSuccess) break;
         AttnArgs at;
@@ -261,6 +272,7 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
         o.bias = c.o_bias ? w.bo : nullptr;
         o.batch = M;
         stream_output(m, o, w.ln2);
+        if (xl) o.xl_out = m->xl_h;
         if (decode && M == 1 && attn_o_fusable(c.wfmt, at, o)) {
             // batch 1, short context: attention, O projection and residual add in one launch
             e = timed(m, BH_K_ATTN_O, [&] { return launch_attn_o(c.wfmt, at, o, st); });
@@ -279,6 +291,10 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
         gu.y = m->mm;
         gu.ldy = I;
         gu.batch = M;
+        if (xl) {
+            gu.xl = m->xl_h;
+            gu.xl_out = m->xl_f;
+        }
         e = timed(m, BH_K_GEMV_GATEUP, [&] { return launch_gemv(c.wfmt, EPI_SILU, gu, st); });
         if (e != hipSuccess) break;
         GemvArgs d;
@@ -287,6 +303,10 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
         d.ldx = I;
         d.batch = M;
         stream_output(m, d, l + 1 < c.n_layers ? m->L[l + 1].ln1 : m->norm);  // final norm after the last layer
+        if (xl) {
+            d.xl = m->xl_f;
+            d.xl_out = m->xl_h;
+        }
         if (decode && l + 1 == c.n_layers && lm_presplit(m, M)) d.xw_hl = m->xw_hl;
         e = timed(m, BH_K_GEMV_DOWN, [&] { return launch_gemv(c.wfmt, EPI_RESNORM, d, st); });
     }
@@ -302,6 +322,7 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
     lm.pen = m->d_pen;
     lm.n_slots = c.max_seqs;
     if (lm_presplit(m, M)) lm.x_hl = m->xw_hl;
+    if (xl) lm.xl = m->xl_h;
     lm.vocab = c.vocab;
     lm.slot = slot;
     lm.part_val = m->part_val;
@@ -330,6 +351,7 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
     sa.xw = m->xw;
     sa.ssq = m->ssq;
     sa.ssq_tiles = m->ssq_tiles;
+    if (xl) sa.xl = m->xl_h;
     return timed(m, BH_K_OTHER, [&] { return launch_sample(sa, st); });
 }
 
@@ -337,7 +359,7 @@ hipError_t forward(bh_model* m, int M, bool decode, int splits, int split_rows) 
 hipError_t decode_start(bh_model* m) {
     return timed(m, BH_K_OTHER, [&] {
         return launch_embed(m->embed, m->d_tok, m->L[0].ln1, m->x, m->xw, m->ssq, m->ssq_tiles, m->d_step, m->B,
-                            m->st);
+                            m->st, use_xl(m, m->B) ? m->xl_h : nullptr);
     });
 }
 
@@ -517,6 +539,8 @@ int bh_model_create(bh_ctx* ctx, const bh_model_config* cfg, bh_model** out) {
         {(void**)&m->d_ids, (size_t)m->ids_steps * DB * 4},
         {(void**)&m->d_pen, (size_t)c.max_seqs * c.vocab * 2},
         {(void**)&m->xw_hl, DB * c.hidden * 4},
+        {(void**)&m->xl_h, (size_t)(c.hidden + 31) / 32 * (XL_REC_BYTES + 4)},
+        {(void**)&m->xl_f, (size_t)(c.ffn + 31) / 32 * (XL_REC_BYTES + 4)},
     };
     for (auto& b : bufs)
         if ((e = dmalloc(m, b.p, b.bytes)) != hipSuccess) return bail(e, "hipMalloc(activations)");
@@ -790,7 +814,8 @@ int bh_model_prefill(bh_model* m, int slot, const uint32_t* tokens, int n) {
         int splits, rows;
         attn_plan(pos[M - 1] + 1, M, m->c.n_kv_heads, m->c.head_dim, &splits, &rows);
         if (e == hipSuccess)
-            e = launch_embed(m->embed, m->d_ptok, m->L[0].ln1, m->x, m->xw, m->ssq, m->ssq_tiles, nullptr, M, m->st);
+            e = launch_embed(m->embed, m->d_ptok, m->L[0].ln1, m->x, m->xw, m->ssq, m->ssq_tiles, nullptr, M, m->st,
+                             use_xl(m, M) ? m->xl_h : nullptr);
         if (e == hipSuccess) e = forward(m, M, false, splits, rows);
         if (e == hipSuccess) e = hipStreamSynchronize(m->st);  // the staging buffer is reused next chunk
         if (e != hipSuccess) return m->ctx->hip_fail(e, "prefill");

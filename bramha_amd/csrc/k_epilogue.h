@@ -9,6 +9,7 @@
 #include <hip/hip_fp16.h>
 
 #include "bh_internal.h"
+#include "k_xl.h"
 
 namespace bh {
 
@@ -400,21 +401,23 @@ struct EpiPre {
 
 // run_epilogue's batch-1 EPI_RESNORM for one 64-row tile finished by one wave whose lane r
 // holds row row0 + r's sum (and loaded its operands into `pre`): x += acc + bias, xw = x * w_next,
-// the tile's sum of squares, all in registers.
+// the tile's sum of squares, all in registers; with a.xl_out also xw's limb records.
 template <int FMT>
 __device__ __forceinline__ void resnorm_wave(const GemvArgs& a, float sum, int64_t row0, const EpiPre<EPI_RESNORM>& pre) {
     const int lane = threadIdx.x & 63;
     const int64_t nn = row0 + lane;
-    float sq = 0.f;
+    float sq = 0.f, xw = 0.f;
     if (nn < a.N) {
         const float v = pre.x0 + (sum * row_scale<FMT>(a.S, nn) + pre.bias);
         a.y[nn] = v;
-        a.xw_out[nn] = v * pre.w1;
+        xw = v * pre.w1;
+        a.xw_out[nn] = xw;
         sq = v * v;
     }
     const float t = wave_sum64(sq);
     const int64_t tile = row0 / 64;
     if (lane == 0 && tile < a.ssq_tiles) a.ssq_out[tile] = t;
+    if (a.xl_out) xl_pack64(xw, a.xl_out, row0 / 32, (a.N + 31) / 32);
 }
 
 // Row offset of row nn's rotate-half RoPE partner (+- hd/2 within its head).
@@ -477,11 +480,15 @@ __device__ __forceinline__ void run_epilogue(const GemvArgs& a, const float* fin
                 static_assert(ROWS == 64, "one wave finishes a 64-row tile");
                 if (threadIdx.x < 64) resnorm_wave<FMT>(a, fin[threadIdx.x], row0, *pre);
             } else if constexpr (EPI == EPI_SILU) {
+                float y = 0.f;
                 if (ok) {
                     const float g = fin[rr] * row_scale<FMT>(a.S, nn) * rn[0];
                     const float u = fin[ROWS + rr] * row_scale<FMT>(a.S2, nn) * rn[0];
-                    a.y[nn] = g * (1.0f / (1.0f + expf(-g))) * u;
+                    y = g * (1.0f / (1.0f + expf(-g))) * u;
+                    a.y[nn] = y;
                 }
+                // wave 0 holds the tile's 64 rows: their limb records for the down projection
+                if (ROWS == 64 && a.xl_out && threadIdx.x < 64) xl_pack64(y, a.xl_out, row0 / 32, (a.N + 31) / 32);
             } else if constexpr (EPI == EPI_QKV) {
                 if (ok) qkv_row<FMT>(a, nn, fin[rr], fin[rr + qkv_partner(a, nn)], rn[0], *pre);
             } else if constexpr (EPI == EPI_LMHEAD) {

@@ -11,6 +11,8 @@
 // results are deterministic without atomics.
 // Epilogues fuse the RMSNorm factor, bias, residual add (with the next norm's inputs),
 // SiLU gate, RoPE + KV-cache append, and the LM-head repetition penalty + argmax.
+// Batch-1 group-32 passes whose activations come as int4 limb records (k_xl.h) take each chunk as
+// 24 integer dots (v_dot8_i32_i4) instead of 32 converts and 32 FMAs.
 #include "bh_internal.h"
 
 #include <hip/hip_fp16.h>
@@ -23,7 +25,7 @@
 namespace bh {
 namespace {
 
-template <int FMT, int B, int EPI, int RW, int U, int CP>
+template <int FMT, int B, int EPI, int RW, int U, int CP, bool XL>
 __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
     extern __shared__ float smem[];
     float* rn = smem;          // [32] per-token norm factors
@@ -61,10 +63,11 @@ __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
         float acc[NACC][B];
         float touch[TOUCH_ROWS];
         RnormLanes<B, (B <= 4 ? RN_U : 8)> rq;
-        stream_chunks<FMT, B, NACC, U, CP>(a, nl, c0, c1, acc, [&] {
+        stream_chunks<FMT, B, NACC, U, CP, XL>(a, nl, c0, c1, acc, [&] {
             // the activation touch (bs1 decode step: 1232 -> 1291 tok/s), the norm factors and the
             // batch-1 epilogue operands load while the first weight stage is in flight
-            touch_activations<B, E>(a, wc0, wc1, touch);
+            if constexpr (XL) touch_xl(a, wc0, wc1, touch);
+            else touch_activations<B, E>(a, wc0, wc1, touch);
             rq.request(a);
             if constexpr (B == 1) pre.load(a, (int64_t)tile * ROWS, ROWS);
         });
@@ -108,7 +111,7 @@ __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
     run_epilogue<FMT, B, EPI, ROWS>(a, comb, comb + TOT, rn, (int64_t)tile * ROWS, B == 1 ? &pre : nullptr);
 }
 
-template <int FMT, int B, int EPI, int RW, int U>
+template <int FMT, int B, int EPI, int RW, int U, bool XL = false>
 hipError_t launch_one(const GemvArgs& a, int ksplit, hipStream_t st) {
     constexpr int NACC = EPI == EPI_SILU ? 2 : 1;
     constexpr int ROWS = 64 * RW;
@@ -119,11 +122,20 @@ hipError_t launch_one(const GemvArgs& a, int ksplit, hipStream_t st) {
     // non-temporal weight loads pay off on weights far larger than the caches (LM head: 20 us
     // instead of 22) and cost latency-bound small ones ~0.2 us
     if (FMT == BH_Q4_G32 && (size_t)a.C * a.n_pad * 16 >= STREAM_BYTES)
-        launch_kernel((k_gemv<FMT, B, EPI, RW, U, FMT == BH_Q4_G32 ? CPOL_STREAM : 0>), dim3(tiles), dim3(64 * RW * ksplit),
-                      shm, st, a);
+        launch_kernel((k_gemv<FMT, B, EPI, RW, U, FMT == BH_Q4_G32 ? CPOL_STREAM : 0, XL>), dim3(tiles),
+                      dim3(64 * RW * ksplit), shm, st, a);
     else
-        launch_kernel((k_gemv<FMT, B, EPI, RW, U, 0>), dim3(tiles), dim3(64 * RW * ksplit), shm, st, a);
+        launch_kernel((k_gemv<FMT, B, EPI, RW, U, 0, XL>), dim3(tiles), dim3(64 * RW * ksplit), shm, st, a);
     return hipGetLastError();
+}
+
+// The batch-1 group-32 pass with limb activations (a.xl set): the same stage depths.
+template <int EPI, int RW>
+hipError_t launch_xl(const GemvArgs& a, int ksplit, int cpw, hipStream_t st) {
+    constexpr int NACC = EPI == EPI_SILU ? 2 : 1;
+    if (cpw <= 2) return launch_one<BH_Q4_G32, 1, EPI, RW, 2, true>(a, ksplit, st);
+    if (cpw <= 12 || NACC == 2) return launch_one<BH_Q4_G32, 1, EPI, RW, 4, true>(a, ksplit, st);
+    return launch_one<BH_Q4_G32, 1, EPI, RW, 8 / NACC, true>(a, ksplit, st);
 }
 
 // Stage depth from the chunks each wave streams (cpw): a single stage covers short ranges,
@@ -131,6 +143,8 @@ hipError_t launch_one(const GemvArgs& a, int ksplit, hipStream_t st) {
 template <int FMT, int EPI, int RW>
 hipError_t launch_b(const GemvArgs& a, int B, int ksplit, int cpw, hipStream_t st) {
     constexpr int NACC = EPI == EPI_SILU ? 2 : 1;
+    if constexpr (FMT == BH_Q4_G32)
+        if (B == 1 && a.xl) return launch_xl<EPI, RW>(a, ksplit, cpw, st);
     if (B <= 2) {
         const bool b1 = B == 1;
         if (cpw <= 2) return b1 ? launch_one<FMT, 1, EPI, RW, 2>(a, ksplit, st) : launch_one<FMT, 2, EPI, RW, 2>(a, ksplit, st);
@@ -158,7 +172,23 @@ hipError_t launch_fmt(int epi, const GemvArgs& a, int B, int rw, int ksplit, int
     }
 }
 
+// Limb records (k_xl.h) of one activation row of n elements: a wavefront per 64 elements
+// (elements past n count as zero), records of chunks [0, ceil(n / 32)).
+__global__ void __launch_bounds__(256) k_xl_pack(const float* x, int n, uint32_t* rec) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t base = i & ~(int64_t)63;
+    if (base >= n) return;  // whole wavefronts
+    const float v = i < n ? x[i] : 0.f;
+    xl_pack64(v, rec, base / 32, (n + 31) / 32);
+}
+
 }  // namespace
+
+hipError_t launch_xl_pack(const float* x, int n, uint32_t* rec, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    launch_kernel(k_xl_pack, dim3((n + 255) / 256), dim3(256), 0, st, x, n, rec);
+    return hipGetLastError();
+}
 
 // Waves per workgroup along K: aim for ~32 waves per CU and >= 2 chunks per wave; the combine
 // area stays under 60 KB. (Measured on the 151936 x 896 LM head: 4 waves per row tile stream
@@ -253,6 +283,16 @@ hipError_t launch_gemv(int fmt, int epi, const GemvArgs& a0, hipStream_t st) {
         if (mf && rem > 32 && epi != EPI_LMHEAD) B = (rem + 15) / 16 * 16;
         GemvArgs a = gemv_tokens(a0, b0, mf ? std::min(B, rem) : B);
         hipError_t e;
+        if (B == 1 && !mf && fmt == BH_Q4_G32) {
+            if (b0 > 0) a.xl = nullptr;  // a producer's records describe token 0
+            if (!a.xl && a.xl_tmp) {     // the caller has x only: its records first
+                e = launch_xl_pack(a.x, a.C * 32, a.xl_tmp, st);
+                if (e != hipSuccess) return e;
+                a.xl = a.xl_tmp;
+            }
+        } else {
+            a.xl = nullptr;
+        }
         if (mf && epi == EPI_LMHEAD && fmt == BH_Q4_G32 && lmhead_mf_fits(a, device_cus())) {
             e = launch_lmhead_mf(a, device_cus(), st);
         } else if (mf) {

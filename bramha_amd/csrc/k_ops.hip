@@ -3,6 +3,8 @@
 
 #include <hip/hip_fp16.h>
 
+#include "k_xl.h"
+
 namespace bh {
 namespace {
 
@@ -97,35 +99,37 @@ __device__ __forceinline__ float embed_elem(const DevWeight& t, int64_t id, int 
 }
 
 // Residual stream of token row b from embedding row `id`: x, xw = x * w0, and per-64-element
-// sums of squares (one wave per tile, a fixed shuffle order).
+// sums of squares (one wave per tile, a fixed shuffle order); with xl, xw's limb records too.
 __device__ __forceinline__ void embed_stream(const DevWeight& t, int64_t id, const float* w0, float* x, float* xw,
-                                             float* ssq, int ssq_tiles, int b) {
+                                             float* ssq, int ssq_tiles, int b, uint32_t* xl) {
     const int hidden = (int)t.k;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     float* xr = x + (int64_t)b * hidden;
     float* xwr = xw + (int64_t)b * hidden;
     for (int tl = wave; tl < ssq_tiles; tl += nw) {
         const int i = tl * 64 + lane;
-        float v = 0.f;
+        float v = 0.f, vw = 0.f;
         if (i < hidden) {
             v = embed_elem(t, id, i);
             xr[i] = v;
-            xwr[i] = v * w0[i];
+            vw = v * w0[i];
+            xwr[i] = vw;
         }
         float sq = v * v;
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
         if (lane == 0) ssq[(int64_t)b * ssq_tiles + tl] = sq;
+        if (xl) xl_pack64(vw, xl, 2 * tl, (hidden + 31) / 32);
     }
 }
 
 __global__ void __launch_bounds__(256) k_embed(const DevWeight t, const int32_t* __restrict__ tok,
                                                const float* __restrict__ w0, float* x, float* xw, float* ssq,
-                                               int ssq_tiles, int32_t* reset_step) {
+                                               int ssq_tiles, int32_t* reset_step, uint32_t* xl) {
     const int b = blockIdx.x;
     const int64_t id = (int64_t)((uint32_t)tok[b] % (uint64_t)t.n);
     if (reset_step && threadIdx.x == 0) reset_step[b] = 0;
-    embed_stream(t, id, w0, x, xw, ssq, ssq_tiles, b);
+    embed_stream(t, id, w0, x, xw, ssq, ssq_tiles, b, b == 0 ? xl : nullptr);
 }
 
 // End of a decode step for batch entry b = blockIdx.x: the first-max argmax over the LM head's
@@ -252,7 +256,7 @@ __global__ void __launch_bounds__(SAMPLE_THREADS) k_sample(const SampleArgs a, c
             a.tok[b] = idx;
             a.pos[b] = a.pos[b] + 1;
         }
-        embed_stream(t, idx, a.w0, a.x, a.xw, a.ssq, a.ssq_tiles, b);
+        embed_stream(t, idx, a.w0, a.x, a.xw, a.ssq, a.ssq_tiles, b, b == 0 ? a.xl : nullptr);
         return;
     }
     // Greedy. What does not depend on the chosen id is requested first, in one round of loads:
@@ -316,18 +320,21 @@ __global__ void __launch_bounds__(SAMPLE_THREADS) k_sample(const SampleArgs a, c
     // next step's residual stream from the embedding row (embed_stream with the weights loaded)
     float* xr = a.x + (int64_t)b * hidden;
     float* xwr = a.xw + (int64_t)b * hidden;
+    uint32_t* xl = b == 0 ? a.xl : nullptr;
     auto put = [&](int tl, float w) {
         const int i = tl * 64 + lane;
-        float e = 0.f;
+        float e = 0.f, ew = 0.f;
         if (i < hidden) {
             e = embed_elem(t, id, i);
             xr[i] = e;
-            xwr[i] = e * w;
+            ew = e * w;
+            xwr[i] = ew;
         }
         float sq = e * e;
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
         if (lane == 0) a.ssq[(int64_t)b * a.ssq_tiles + tl] = sq;
+        if (xl) xl_pack64(ew, xl, 2 * tl, (hidden + 31) / 32);
     };
 #pragma unroll
     for (int k = 0; k < EW; ++k)
@@ -425,10 +432,10 @@ hipError_t launch_dequant(const DevWeight& w, float* out, hipStream_t st) {
 }
 
 hipError_t launch_embed(const DevWeight& t, const int32_t* tok, const float* w0, float* x, float* xw, float* ssq,
-                        int ssq_tiles, int32_t* reset_step, int batch, hipStream_t st) {
+                        int ssq_tiles, int32_t* reset_step, int batch, hipStream_t st, uint32_t* xl) {
     if (batch <= 0) return hipSuccess;
     if (ssq_tiles != (int)((t.k + 63) / 64)) return hipErrorInvalidValue;
-    launch_kernel(k_embed, dim3(batch), dim3(256), 0, st, t, tok, w0, x, xw, ssq, ssq_tiles, reset_step);
+    launch_kernel(k_embed, dim3(batch), dim3(256), 0, st, t, tok, w0, x, xw, ssq, ssq_tiles, reset_step, xl);
     return hipGetLastError();
 }
 

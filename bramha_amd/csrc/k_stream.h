@@ -12,6 +12,7 @@
 #include <hip/hip_fp16.h>
 
 #include "bh_internal.h"
+#include "k_xl.h"
 
 namespace bh {
 
@@ -70,14 +71,15 @@ __device__ __forceinline__ void decode(const uint4 q, float* v) {
 
 // acc[j][b] += sum over chunks [c0, c1) of weight j's row nl against activation row b of a.x
 // (a.W / a.S, and a.W2 / a.S2 for NACC == 2). `mid()` runs once the first stage of loads is in
-// flight: whatever it loads overlaps the weight latency.
+// flight: whatever it loads overlaps the weight latency. XL (batch 1, Q4_G32): the activations
+// are the limb records a.xl (k_xl.h) and each chunk is an integer dot product.
 //
 // Weight and scale loads are raw buffer loads: an SGPR resource per matrix, the lane's row as
 // the VGPR offset and the chunk as the (uniform) SGPR offset, so a stage costs no per-load
 // address arithmetic. Every load of a stage is unconditional (chunk index clamped to the wave's
 // last chunk, scale kept as raw fp16 bits) so all of a stage's loads are in flight before the
 // first of them is waited on. The chunk loop is software-pipelined over two stages of U chunks.
-template <int FMT, int B, int NACC, int U, int CP, class Mid>
+template <int FMT, int B, int NACC, int U, int CP, bool XL, class Mid>
 __device__ __forceinline__ void stream_chunks(const GemvArgs& a, int64_t nl, int c0, int c1, float (&acc)[NACC][B],
                                               Mid&& mid) {
     constexpr int E = Fmt<FMT>::E;
@@ -112,6 +114,8 @@ __device__ __forceinline__ void stream_chunks(const GemvArgs& a, int64_t nl, int
 #pragma unroll
         for (int b = 0; b < B; ++b) acc[j][b] = 0.f;
 
+    if constexpr (XL) static_assert(FMT == BH_Q4_G32 && B == 1, "limb activations: batch-1 group-32 passes");
+
     // Chunks past c1 (clamped re-reads of the last one) are skipped by a uniform branch that
     // holds no vector loads, so the loads' wait counts are unaffected by it.
     auto consume = [&](int c, const uint4 (&q)[NACC][U], const uint32_t (&s)[NACC][U]) {
@@ -119,6 +123,15 @@ __device__ __forceinline__ void stream_chunks(const GemvArgs& a, int64_t nl, int
         for (int u = 0; u < U; ++u) {
             if (c + u < c1) {
                 const int kb = (c + u) * E;
+                if constexpr (XL) {
+                    const uint32_t* xr = a.xl + (int64_t)(c + u) * XL_REC;
+                    const float f = __uint_as_float(a.xl[(int64_t)a.C * XL_REC + c + u]);
+#pragma unroll
+                    for (int j = 0; j < NACC; ++j)
+                        acc[j][0] = fmaf(xl_dot_chunk(q[j][u], xr, f), __half2float(__ushort_as_half((uint16_t)s[j][u])),
+                                         acc[j][0]);
+                    continue;
+                }
 #pragma unroll
                 for (int j = 0; j < NACC; ++j) {
                     float v[E];
@@ -164,6 +177,13 @@ __device__ __forceinline__ void touch_activations(const GemvArgs& a, int wc0, in
     const int i2 = min((int)threadIdx.x * 32, max(nx - 1, 0));
 #pragma unroll
     for (int bb = 0; bb < TOUCH_ROWS; ++bb) t[bb] = a.x[(int64_t)min(bb, B - 1) * a.ldx + wc0 * E + i2];
+}
+// The same touch for limb records: one 128-byte record per thread.
+__device__ __forceinline__ void touch_xl(const GemvArgs& a, int wc0, int wc1, float (&t)[TOUCH_ROWS]) {
+    const int i = min((int)threadIdx.x, max(wc1 - wc0 - 1, 0));
+    t[0] = __uint_as_float(a.xl[(int64_t)(wc0 + i) * XL_REC]);
+#pragma unroll
+    for (int bb = 1; bb < TOUCH_ROWS; ++bb) t[bb] = 0.f;
 }
 template <int B>
 __device__ __forceinline__ void touch_sink(const float (&t)[TOUCH_ROWS]) {

@@ -80,6 +80,59 @@ def test_gemv_q4g32_qwen_shapes(plane, n, k, batch):
         assert np.max(np.abs(y[0] - yo)) <= 1e-5 * max(1.0, np.abs(yo).max())
 
 
+def _limb_edge_rows(k):
+    """Activation rows that stress the batch-1 group-32 pass, whose activations are turned into
+    8 signed 4-bit limbs under one exponent per 32-element chunk: huge and tiny values in one
+    chunk, outliers 1e4 above their chunk, all-zero chunks, a chunk below the 2^-97 cut, powers
+    of two at the chunk maximum, negative maxima, subnormals, and magnitudes near the f32 limit."""
+    rng = np.random.default_rng(7)
+    rows = []
+    x = rng.standard_normal(k).astype(np.float32)
+    x[0], x[1], x[2] = 1e30, -1e-30, 3e-8
+    x[32:64] = 0.0
+    x[64:96] = 1e-35 * rng.standard_normal(32)
+    rows.append(x)
+    x = rng.standard_normal(k).astype(np.float32)
+    x[3::32] = 1e4 * np.sign(x[3::32])
+    rows.append(x)
+    x = np.zeros(k, np.float32)
+    x[::32] = 2.0 ** np.arange(-60, -60 + k // 32)[: len(x[::32])]   # maxima at powers of two
+    x[5::32] = -x[::32] * 0.75
+    rows.append(x)
+    x = -np.abs(rng.standard_normal(k)).astype(np.float32)            # negative maxima
+    x[7] = -4.0
+    rows.append(x)
+    x = (rng.standard_normal(k) * 1e-39).astype(np.float32)            # subnormal chunks
+    x[::64] = 1e-37
+    rows.append(x)
+    x = (rng.standard_normal(k) * 1e36).astype(np.float32)             # near the top of f32
+    rows.append(x)
+    return rows
+
+
+@pytest.mark.parametrize("n,k", [(300, 128), (896, 896), (4864, 896)])
+def test_gemv_batch1_limb_activations_edge_values(plane, n, k):
+    """The batch-1 group-32 GEMV against the float64 product of the dequantized weights on
+    activations at the edges of the limb encoding, within the bound of the other GEMV tests
+    (2e-6 * |W| |x|) plus the encoding's own: every element rounded to 2^-30 of its chunk's
+    largest magnitude (2^-30 * |W| * chunkmax|x|). A NaN activation makes every output NaN, as
+    in the f32 product."""
+    q, s, deq = _quant(BH_Q4_G32, _w(n + 3 * k, n, k))
+    dw = ops.DeviceWeight(plane, BH_Q4_G32, n, k, q, s)
+    a64 = np.abs(deq).astype(np.float64)
+    for i, x in enumerate(_limb_edge_rows(k)):
+        y = dw.gemv(ops.DeviceArray.from_numpy(plane, x[None, :])).numpy()
+        assert np.isfinite(y).all(), i
+        want = x.astype(np.float64) @ deq.astype(np.float64).T
+        cmax = np.repeat(np.abs(x.astype(np.float64)).reshape(-1, 32).max(axis=1), 32)
+        bound = 2e-6 * (np.abs(x).astype(np.float64) @ a64.T) + 2.0 ** -30 * (cmax @ a64.T) + 1e-7
+        assert np.all(np.abs(y[0] - want) <= bound), (i, float((np.abs(y[0] - want) / bound).max()))
+    x = np.random.default_rng(1).standard_normal(k).astype(np.float32)
+    x[k // 2] = np.nan
+    y = dw.gemv(ops.DeviceArray.from_numpy(plane, x[None, :])).numpy()
+    assert np.isnan(y).all()
+
+
 @pytest.mark.parametrize("fmt", [BH_Q4_G32, BH_Q4_ROW])
 @pytest.mark.parametrize("n,k", [(37, 96), (300, 96), (1000, 896)])
 @pytest.mark.parametrize("batch", [1, 9, 16, 32, 40, 63])
