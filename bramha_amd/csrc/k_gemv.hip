@@ -129,13 +129,16 @@ hipError_t launch_one(const GemvArgs& a, int ksplit, hipStream_t st) {
     return hipGetLastError();
 }
 
-// The batch-1 group-32 pass with limb activations (a.xl set): the same stage depths.
+// The batch-1 group-32 pass with limb activations (a.xl set). With the integer dots the loop
+// waits on loads, not on arithmetic, and shallow stages keep more wavefronts resident: stages of
+// 2 chunks, 1 for the gate/up pair and QKV (measured in the Qwen2-7B-width decode step: LM head
+// 57 -> 50 us with 8 waves per tile, gate/up 22.2 -> 19.1, down 12.1 -> 10.8, QKV 8.0 -> 7.7;
+// Qwen2-0.5B LM head 17.6 -> 15.9, gate/up 5.2 -> 4.8, QKV 4.8 -> 4.5).
 template <int EPI, int RW>
 hipError_t launch_xl(const GemvArgs& a, int ksplit, int cpw, hipStream_t st) {
     constexpr int NACC = EPI == EPI_SILU ? 2 : 1;
-    if (cpw <= 2) return launch_one<BH_Q4_G32, 1, EPI, RW, 2, true>(a, ksplit, st);
-    if (cpw <= 12 || NACC == 2) return launch_one<BH_Q4_G32, 1, EPI, RW, 4, true>(a, ksplit, st);
-    return launch_one<BH_Q4_G32, 1, EPI, RW, 8 / NACC, true>(a, ksplit, st);
+    if (cpw <= 1 || NACC == 2 || EPI == EPI_QKV) return launch_one<BH_Q4_G32, 1, EPI, RW, 1, true>(a, ksplit, st);
+    return launch_one<BH_Q4_G32, 1, EPI, RW, 2, true>(a, ksplit, st);
 }
 
 // Stage depth from the chunks each wave streams (cpw): a single stage covers short ranges,
@@ -305,7 +308,11 @@ hipError_t launch_gemv(int fmt, int epi, const GemvArgs& a0, hipStream_t st) {
         } else {
             a.ksw = auto_splits(a0, epi, false, 64 * rw, nacc * B * 64 * rw);
             const int tiles = (a0.n_pad + 64 * rw - 1) / (64 * rw);
-            const int ks = waves_per_tile(tiles * a.ksw, rw, (a0.C + a.ksw - 1) / a.ksw, nacc, B);
+            int ks = waves_per_tile(tiles * a.ksw, rw, (a0.C + a.ksw - 1) / a.ksw, nacc, B);
+            if (B == 1 && a.xl) {  // limb passes (launch_xl): LM heads ~14 chunks per wave, QKV <= 8 waves
+                if (epi == EPI_LMHEAD) ks = std::max(4, std::min(a0.C / 14, 12));
+                else if (epi == EPI_QKV) ks = std::min(ks, 8);
+            }
             const int cpw = ((a0.C + a.ksw - 1) / a.ksw + ks - 1) / ks;  // chunks per wave
             switch (fmt) {
                 case BH_F32: e = launch_fmt<BH_F32>(epi, a, B, rw, ks, cpw, st); break;
