@@ -134,11 +134,11 @@ def test_gemv_batch1_limb_activations_edge_values(plane, n, k):
 
 
 @pytest.mark.parametrize("n,k", [(18944, 3584), (3584, 18944), (37000, 1024), (9999, 4096)])
-def test_gemv_batch1_stream_k_large(plane, n, k):
-    """Batch-1 group-32 GEMVs of 16 MiB and more (the stream-K launch: equal ranges of
-    (tile, chunk) units per wavefront, partial sums of a tile added in range order) against the
-    float64 product, at 7B projection shapes and shapes whose ranges split tiles unevenly; a
-    second launch gives bit-identical results."""
+def test_gemv_batch1_large_limb(plane, n, k):
+    """Batch-1 group-32 GEMVs of 16 MiB and more on limb activations (K split over workgroups,
+    partial sums of a tile added in split order) against the float64 product, at Qwen2-7B
+    projection shapes and shapes whose K does not divide evenly into the splits; a second launch
+    gives bit-identical results."""
     q, s, deq = _quant(BH_Q4_G32, _w(n + k, n, k))
     dw = ops.DeviceWeight(plane, BH_Q4_G32, n, k, q, s)
     x = np.random.default_rng(n).standard_normal((1, k)).astype(np.float32)
