@@ -239,7 +239,8 @@ def ragged_decode(plane, n_seq=32, lo=128, hi=8192, steps=128, new_prompt=64, ma
     id or at its own output length, drawn uniformly from [16, steps] by seed (requests of unequal
     length); an ended sequence is replaced in its batch entry by a new one with a
     `new_prompt`-token random prompt, prefilled inside the timed loop into the ended sequence's
-    KV region (its slot reopened), so the captured decode step stays valid. Only tokens of live
+    KV region (its slot reopened), so the captured decode step stays valid; the prompts of the
+    entries that end at the same step are prefilled together (one multi-sequence pass). Only tokens of live
     sequences count. No sink eviction: the reference's prefill cannot pass its 4096-row eviction
     limit (its prefill attention reads evicted rows by absolute position and panics,
     cpu_engine.rs:1166-1170, 1728-1754), so every sequence keeps its whole context."""
@@ -286,6 +287,7 @@ def ragged_decode(plane, n_seq=32, lo=128, hi=8192, steps=128, new_prompt=64, ma
         td = time.perf_counter()
         ids = m.decode(k)
         t_decode += time.perf_counter() - td
+        refill = []
         for b in range(n_seq):
             hit = np.nonzero(np.isin(ids[:, b], EOS_IDS))[0]
             n_ok = min(int(hit[0]) + 1 if hit.size else k, int(left[b]))
@@ -293,13 +295,18 @@ def ragged_decode(plane, n_seq=32, lo=128, hi=8192, steps=128, new_prompt=64, ma
             left[b] -= k
             ctx_len[b] += k
             if (hit.size or left[b] <= 0) and done + k < steps:
-                p = synth_tokens(seed, "ragged.new.%d" % replaced, new_prompt, cfg.vocab)
-                m.seq_open(b, new_prompt + steps + 16)  # the entry's own slot: same KV region
-                m.prefill(b, p[:-1])
-                m.decode_replace(b, b, int(p[-1]))
+                refill.append((b, synth_tokens(seed, "ragged.new.%d" % replaced, new_prompt, cfg.vocab)))
                 replaced += 1
                 left[b] = rng.integers(16, steps + 1)
                 ctx_len[b] = new_prompt
+        if refill:
+            # the prompts of the entries that ended together are prefilled in one pass, each into
+            # its entry's own slot reopened (same KV region: the captured step stays valid)
+            for b, _ in refill:
+                m.seq_open(b, new_prompt + steps + 16)
+            m.prefill_batch([b for b, _ in refill], [p[:-1] for _, p in refill])
+            for b, p in refill:
+                m.decode_replace(b, b, int(p[-1]))
         done += k
     ops.synchronize(plane)
     dt = time.perf_counter() - t0

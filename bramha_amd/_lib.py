@@ -109,6 +109,7 @@ _PROTOS = {
     "bh_model_missing": (c_int, [_P, POINTER(c_int)]),
     "bh_model_seq_open": (c_int, [_P, c_int, c_int64]),
     "bh_model_prefill": (c_int, [_P, c_int, _P, c_int]),
+    "bh_model_prefill_batch": (c_int, [_P, c_int, _P, _P, _P]),
     "bh_model_decode_setup": (c_int, [_P, c_int, _P, _P]),
     "bh_model_decode_replace": (c_int, [_P, c_int, c_int, c_uint32]),
     "bh_model_decode": (c_int, [_P, c_int, _P, _P]),

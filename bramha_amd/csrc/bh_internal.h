@@ -205,7 +205,9 @@ hipError_t launch_gemv(int fmt, int epi, const GemvArgs& a, hipStream_t st);
 hipError_t launch_xl_pack(const float* x, int n, uint32_t* rec, hipStream_t st);
 constexpr int XL_TMP_CHUNKS = 4096;  // chunks of the single-op entry points' record scratch
 constexpr int XL_REC_BYTES = 128;    // bytes of one chunk's limb record (plus 4 of its factor)
-// MFMA GEMM pass of B = 16 or 32 tokens over 4-bit weights (k_gemm.hip), rw * 64 rows per tile.
+// MFMA GEMM pass of B = 16 or 32 tokens over 4-bit weights (k_gemm.hip), rw * 64 rows per tile;
+// B = 48 .. MF_GROUPED_MAX (multiples of 16): B / 16 groups of 16 tokens in one launch.
+constexpr int MF_GROUPED_MAX = 512;
 hipError_t launch_gemm_mf(int fmt, int epi, const GemvArgs& a, int B, int rw, hipStream_t st);
 // MFMA GEMM over all a.batch tokens at once for prefill chunks (k_prefill.hip): 128-row by
 // 128-token tiles (64 tokens for the gate/up pair). Not for EPI_LMHEAD.
@@ -294,8 +296,10 @@ struct AttnArgs {
     const int32_t* seq_len = nullptr;  // standalone mode: explicit lengths [batch] (pos unused)
     int batch = 0, nq = 0, nkv = 0, hd = 0;
     int splits = 1, split_rows = 0;    // context split: rows per split (multiple of 64)
-    // prefill: the batch rows are consecutive tokens of one sequence starting at KV row boff[0]
-    // (fp16 cache: one workgroup per 16 tokens and query head; splits unused)
+    // prefill: the batch rows are prompt tokens at their positions pos[b] in the regions boff[b]
+    // (fp16 cache: one workgroup per 16 consecutive rows and query head, the 16 rows of one
+    // sequence — a prefill of several sequences pads each to a multiple of 16 rows with pad rows
+    // at position -1, which attend to nothing and write no KV row; splits unused)
     int prefill = 0;
     float* part_o = nullptr;           // [batch][nq][splits][hd]
     float* part_ml = nullptr;          // [batch][nq][splits][2]

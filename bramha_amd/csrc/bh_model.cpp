@@ -779,13 +779,17 @@ int bh_model_seq_len(bh_model* m, int slot, int64_t* len) {
     return BH_OK;
 }
 
-int bh_model_prefill(bh_model* m, int slot, const uint32_t* tokens, int n) {
-    if (!m || (n > 0 && !tokens)) return BH_ERR_INVALID;
-    std::lock_guard<std::mutex> g(m->ctx->mu);
+namespace {
+
+// One staged prompt row of a prefill chunk: region offset, token, position (-1: a pad row), slot.
+struct PfRow {
+    int64_t boff;
+    int32_t tok, pos, slot;
+};
+
+// Checks of a prefill of n tokens into `slot` (open, positions within the RoPE table, capacity).
+int prefill_check(bh_model* m, int slot, int64_t n) {
     if (slot < 0 || slot >= m->c.max_seqs || !m->open_h[slot]) return m->fail(BH_ERR_INVALID, "slot is not open");
-    int missing = 0;
-    bh_model_missing(m, &missing);
-    if (missing) return m->fail(BH_ERR_INVALID, std::to_string(missing) + " tensors not set");
     const int64_t end = m->len_h[slot] + n;
     if (end > m->max_pos) return m->fail(BH_ERR_CAPACITY, "position beyond the RoPE table");
     if (m->c.max_context > 0) {
@@ -794,34 +798,96 @@ int bh_model_prefill(bh_model* m, int slot, const uint32_t* tokens, int n) {
     } else if (end > m->cap_h[slot]) {
         return m->fail(BH_ERR_CAPACITY, "prefill exceeds the slot's KV capacity");
     }
-    int done = 0;
-    while (done < n) {
-        const int M = std::min(n - done, m->c.max_tokens);
+    return BH_OK;
+}
+
+// Run staged rows through the model in chunks of at most `chunk` rows (the caller's rows keep
+// every 16-row group of an fp16-cache chunk inside one sequence when `chunk` is a multiple of 16).
+int prefill_rows(bh_model* m, const std::vector<PfRow>& rows, int chunk) {
+    size_t done = 0;
+    while (done < rows.size()) {
+        const int M = (int)std::min<size_t>(rows.size() - done, (size_t)chunk);
         int64_t* bo = (int64_t*)m->h_stage;
         int32_t* tok = (int32_t*)(bo + M);
         int32_t* pos = tok + M;
         int32_t* sl = pos + M;
+        int maxpos = 0;
         for (int i = 0; i < M; ++i) {
-            bo[i] = m->off_h[slot];
-            tok[i] = (int32_t)tokens[done + i];
-            pos[i] = m->len_h[slot] + done + i;
-            sl[i] = slot;
+            const PfRow& r = rows[done + i];
+            bo[i] = r.boff;
+            tok[i] = r.tok;
+            pos[i] = r.pos;
+            sl[i] = r.slot;
+            maxpos = std::max(maxpos, r.pos);
         }
         hipError_t e = hipMemcpyAsync(m->d_pboff, bo, (size_t)M * 8, hipMemcpyHostToDevice, m->st);
         if (e == hipSuccess) e = hipMemcpyAsync(m->d_ptok, tok, (size_t)M * 4, hipMemcpyHostToDevice, m->st);
         if (e == hipSuccess) e = hipMemcpyAsync(m->d_ppos, pos, (size_t)M * 4, hipMemcpyHostToDevice, m->st);
         if (e == hipSuccess) e = hipMemcpyAsync(m->d_pslot, sl, (size_t)M * 4, hipMemcpyHostToDevice, m->st);
-        int splits, rows;
-        attn_plan(pos[M - 1] + 1, M, m->c.n_kv_heads, m->c.head_dim, &splits, &rows);
+        int splits, srows;
+        attn_plan(maxpos + 1, M, m->c.n_kv_heads, m->c.head_dim, &splits, &srows);
         if (e == hipSuccess)
             e = launch_embed(m->embed, m->d_ptok, m->L[0].ln1, m->x, m->xw, m->ssq, m->ssq_tiles, nullptr, M, m->st,
                              use_xl(m, M) ? m->xl_h : nullptr);
-        if (e == hipSuccess) e = forward(m, M, false, splits, rows);
+        if (e == hipSuccess) e = forward(m, M, false, splits, srows);
         if (e == hipSuccess) e = hipStreamSynchronize(m->st);  // the staging buffer is reused next chunk
         if (e != hipSuccess) return m->ctx->hip_fail(e, "prefill");
         done += M;
     }
+    return BH_OK;
+}
+
+}  // namespace
+
+int bh_model_prefill(bh_model* m, int slot, const uint32_t* tokens, int n) {
+    if (!m || n < 0 || (n > 0 && !tokens)) return BH_ERR_INVALID;
+    std::lock_guard<std::mutex> g(m->ctx->mu);
+    int missing = 0;
+    bh_model_missing(m, &missing);
+    if (missing) return m->fail(BH_ERR_INVALID, std::to_string(missing) + " tensors not set");
+    int rc = prefill_check(m, slot, n);
+    if (rc) return rc;
+    std::vector<PfRow> rows((size_t)n);
+    for (int i = 0; i < n; ++i) rows[i] = PfRow{m->off_h[slot], (int32_t)tokens[i], (int32_t)(m->len_h[slot] + i), slot};
+    rc = prefill_rows(m, rows, m->c.max_tokens);
+    if (rc) return rc;
     m->len_h[slot] += n;
+    return BH_OK;
+}
+
+int bh_model_prefill_batch(bh_model* m, int n_seqs, const int32_t* slots, const uint32_t* tokens, const int32_t* counts) {
+    if (!m || n_seqs < 0 || (n_seqs > 0 && (!slots || !counts))) return BH_ERR_INVALID;
+    std::lock_guard<std::mutex> g(m->ctx->mu);
+    int missing = 0;
+    bh_model_missing(m, &missing);
+    if (missing) return m->fail(BH_ERR_INVALID, std::to_string(missing) + " tensors not set");
+    int64_t total = 0;
+    for (int s = 0; s < n_seqs; ++s) {
+        if (counts[s] < 0) return m->fail(BH_ERR_INVALID, "negative token count");
+        for (int t = 0; t < s; ++t)
+            if (slots[t] == slots[s]) return m->fail(BH_ERR_INVALID, "a slot appears twice in one batch prefill");
+        const int rc = prefill_check(m, slots[s], counts[s]);
+        if (rc) return rc;
+        total += counts[s];
+    }
+    if (total > 0 && !tokens) return BH_ERR_INVALID;
+    // fp16 cache: every sequence padded to whole 16-row groups (the prefill attention's unit),
+    // chunks of a multiple of 16 rows
+    const int grp = m->c.kv_f16 ? 16 : 1;
+    const int chunk = m->c.kv_f16 ? m->c.max_tokens / 16 * 16 : m->c.max_tokens;
+    if (chunk <= 0) return m->fail(BH_ERR_UNSUPPORTED, "batch prefill needs max_tokens >= 16 with an fp16 cache");
+    std::vector<PfRow> rows;
+    int64_t t0 = 0;
+    for (int s = 0; s < n_seqs; ++s) {
+        const int slot = slots[s], n = counts[s];
+        for (int i = 0; i < n; ++i)
+            rows.push_back(PfRow{m->off_h[slot], (int32_t)tokens[t0 + i], (int32_t)(m->len_h[slot] + i), slot});
+        for (int i = n; i % grp; ++i) rows.push_back(PfRow{m->off_h[slot], 0, -1, slot});
+        t0 += n;
+    }
+    const int rc = prefill_rows(m, rows, chunk);
+    if (rc) return rc;
+    for (int s = 0; s < n_seqs; ++s) m->len_h[slots[s]] += counts[s];
     return BH_OK;
 }
 

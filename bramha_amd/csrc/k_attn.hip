@@ -107,7 +107,7 @@ __device__ __forceinline__ void merge_splits(const AttnArgs& a, int64_t hq0) {
         const int g = i / HD, d = i % HD;
         float O = 0.f;
         for (int s2 = 0; s2 < S; ++s2) O = fmaf(f_s[g][s2], a.part_o[((hq0 + g) * S + s2) * HD + d], O);
-        a.out[(hq0 + g) * HD + d] = O * (1.0f / L_s[g]);
+        a.out[(hq0 + g) * HD + d] = L_s[g] > 0.f ? O * (1.0f / L_s[g]) : 0.f;
     }
 }
 
@@ -271,7 +271,7 @@ __global__ void __launch_bounds__(256) k_attn(const AttnArgs a) {
             O += w_o[w][g][d] * f;
         }
         if (a.splits == 1) {
-            a.out[(hq0 + g) * HD + d] = O * (1.0f / L);
+            a.out[(hq0 + g) * HD + d] = L > 0.f ? O * (1.0f / L) : 0.f;
         } else {
             a.part_o[((hq0 + g) * a.splits + sp) * HD + d] = O;
             if (d == 0) {
@@ -504,7 +504,7 @@ __global__ void __launch_bounds__(64 * NW) k_attn_pf(const AttnArgs a) {
         const int i = threadIdx.x + k * NT;
         qreg[k] = i / HD < ntok ? a.q[((int64_t)(t0 + i / HD) * a.nq + hq) * HD + i % HD] : 0.f;
     }
-    const int64_t off = a.boff[0];  // one sequence per launch
+    const int64_t off = a.boff[t0];  // every 16-token group lies in one sequence
     int lim = 0;
     if (lr < ntok) {
         lim = a.pos[t0 + lr] + 1;

@@ -558,6 +558,10 @@ __device__ __forceinline__ void run_epilogue(const GemvArgs& a, const float* fin
             const int loc = (int)nn - (sec == 0 ? 0 : (sec == 1 ? a.qd : a.qd + a.kd));
             const int hh = loc / a.hd, d = loc % a.hd;
             const int p = a.pos[b];
+            if (p < 0) {  // a pad token of a multi-sequence prefill: no RoPE, no KV row
+                if (sec == 0) a.y[(int64_t)b * a.ldy + nn] = 0.f;
+                continue;
+            }
             if (sec < 2) {  // rotate-half RoPE (apply_rope_cpu, cpu_engine.rs:1682-1699)
                 const int dp = d < half ? half : -half;
                 float pv = fin[i + dp] * row_scale<FMT>(a.S, nn + dp) * rn[b];

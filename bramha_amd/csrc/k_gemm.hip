@@ -322,12 +322,13 @@ hipError_t launch_e(int epi, const GemvArgs& a, int B, int groups, int rw, hipSt
 }  // namespace
 
 hipError_t launch_gemm_mf(int fmt, int epi, const GemvArgs& a, int B, int rw, hipStream_t st) {
-    if ((B != 16 && B != 32 && B != 48 && B != 64) || a.batch < 1 || a.batch > B || a.ksw < 1 || a.n_pad % 64 ||
+    if (B < 16 || B % 16 || B > MF_GROUPED_MAX || a.batch < 1 || a.batch > B || a.ksw < 1 || a.n_pad % 64 ||
         rw < 1 || rw > 2 || (B > 32 && (epi == EPI_LMHEAD || a.batch <= B - 16)))
         return hipErrorInvalidValue;
     if (B > 32) {
-        // 33..64 tokens (a short prefill chunk: a refill's prompt): B / 16 groups of 16 tokens in
-        // one launch, each group its own split scratch region, every group holding a token
+        // 33..MF_GROUPED_MAX tokens (a short prefill chunk: a refill's prompt, or a few of them):
+        // B / 16 groups of 16 tokens in one launch, each group its own split scratch region, every
+        // group holding a token
         const int groups = B / 16;
         const int tiles = (a.n_pad + 64 * rw - 1) / (64 * rw);
         const int tot16 = (epi == EPI_SILU ? 2 : 1) * 16 * 64 * rw;

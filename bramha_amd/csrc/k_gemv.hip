@@ -271,9 +271,23 @@ hipError_t launch_gemv(int fmt, int epi, const GemvArgs& a0, hipStream_t st) {
         const int rem = a0.batch - b0;
         const bool q4 = fmt == BH_Q4_G32 || fmt == BH_Q4_ROW;
         if (q4 && rem >= PF_MIN_TOKENS && epi != EPI_LMHEAD) {
-            // prefill chunk: every remaining token in one tiled launch
+            // prefill chunk: every remaining token in one tiled launch, or, where its 128-row x
+            // 64/128-token tiles would not give every CU a workgroup (narrow matrices, chunks of a
+            // few hundred tokens: a batch of refill prompts), one launch of 16-token MFMA groups
+            // (a 384-token chunk of the 896-wide projections: QKV 85 -> ~15 us)
             GemvArgs a = gemv_tokens(a0, b0, rem);
             a.ksw = 1;
+            const int mt = epi == EPI_SILU ? 64 : 128;
+            const int64_t pf_grid = (int64_t)((rem + mt - 1) / mt) * ((a0.n_pad + 127) / 128);
+            if (rem <= MF_GROUPED_MAX && pf_grid < device_cus()) {
+                const int B = (rem + 15) / 16 * 16;
+                a.ksw = auto_splits(a0, epi, true, 64 * rw, nacc * 16 * 64 * rw);
+                if (a.ksw > 1) {  // every group's split scratch must fit
+                    const int64_t gt = (int64_t)(B / 16) * ((a0.n_pad + 64 * rw - 1) / (64 * rw));
+                    if (gt > SPLIT_TILES_MAX || gt * a.ksw * nacc * 16 * 64 * rw > SPLIT_PART_FLOATS) a.ksw = 1;
+                }
+                return launch_gemm_mf(fmt, epi, a, B, rw, st);
+            }
             return launch_gemm_pf(fmt, epi, a, st);
         }
         // MFMA passes of 16 or 32 token columns; the last pass of more than 8 tokens takes the

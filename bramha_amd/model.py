@@ -218,6 +218,14 @@ class HipDecoder:
         t = np.ascontiguousarray(tokens, dtype=np.uint32)
         self._check(lib.bh_model_prefill(self.m, slot, ptr(t), t.size))
 
+    def prefill_batch(self, slots, token_lists):
+        """Prefill token_lists[i] into slots[i] for every i in one pass (bh_model_prefill_batch)."""
+        s = np.ascontiguousarray(slots, dtype=np.int32)
+        counts = np.array([len(t) for t in token_lists], dtype=np.int32)
+        toks = np.ascontiguousarray(np.concatenate([np.asarray(t, dtype=np.uint32) for t in token_lists])
+                                    if len(token_lists) else np.zeros(0, np.uint32), dtype=np.uint32)
+        self._check(lib.bh_model_prefill_batch(self.m, s.size, ptr(s), ptr(toks), ptr(counts)))
+
     def decode_setup(self, slots, first_tokens):
         s = np.ascontiguousarray(slots, dtype=np.int32)
         t = np.ascontiguousarray(first_tokens, dtype=np.uint32)

@@ -252,6 +252,13 @@ int bh_model_seq_open(bh_model* m, int slot, int64_t capacity);
 /* Run prompt tokens [0, n) of `slot` through the model at its next positions without logits
  * (the reference prefills all prompt tokens but the last, cpu_engine.rs:2586-2757). */
 int bh_model_prefill(bh_model* m, int slot, const uint32_t* tokens, int n);
+/* Prefill several sequences in one pass (no counterpart in the reference, which prefills one
+ * prompt at a time, cpu_engine.rs:2586-2757; for ragged batches that refill several entries at
+ * once): sequence s is counts[s] tokens of `tokens` (concatenated in order) into slots[s], at
+ * that slot's next positions, as bh_model_prefill would run them one by one. Slots must be
+ * distinct and open. */
+int bh_model_prefill_batch(bh_model* m, int n_seqs, const int32_t* slots, const uint32_t* tokens,
+                           const int32_t* counts);
 /* Define the decode batch: batch entry b decodes slot slots[b], whose next input token is
  * first_tokens[b]. */
 int bh_model_decode_setup(bh_model* m, int batch, const int32_t* slots, const uint32_t* first_tokens);

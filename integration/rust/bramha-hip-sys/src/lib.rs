@@ -150,6 +150,8 @@ extern "C" {
     pub fn bh_model_missing(m: *mut bh_model, n_missing: *mut c_int) -> c_int;
     pub fn bh_model_seq_open(m: *mut bh_model, slot: c_int, capacity: i64) -> c_int;
     pub fn bh_model_prefill(m: *mut bh_model, slot: c_int, tokens: *const u32, n: c_int) -> c_int;
+    pub fn bh_model_prefill_batch(m: *mut bh_model, n_seqs: c_int, slots: *const i32, tokens: *const u32,
+        counts: *const i32) -> c_int;
     pub fn bh_model_decode_setup(m: *mut bh_model, batch: c_int, slots: *const i32,
         first_tokens: *const u32) -> c_int;
     pub fn bh_model_decode_replace(m: *mut bh_model, b: c_int, slot: c_int, first_token: u32) -> c_int;

@@ -206,6 +206,20 @@ impl<'p> HipModel<'p> {
         self.status(st)
     }
 
+    /// Several prompts in one pass: `prompts[i]` into `slots[i]` (a ragged batch refilling the
+    /// entries that ended at the same step).
+    pub fn prefill_batch(&mut self, slots: &[i32], prompts: &[&[u32]]) -> Result<(), String> {
+        if slots.len() != prompts.len() {
+            return Err("slots and prompts differ in length".into());
+        }
+        let counts: Vec<i32> = prompts.iter().map(|p| p.len() as i32).collect();
+        let tokens: Vec<u32> = prompts.iter().flat_map(|p| p.iter().copied()).collect();
+        let st = unsafe {
+            sys::bh_model_prefill_batch(self.m, slots.len() as c_int, slots.as_ptr(), tokens.as_ptr(), counts.as_ptr())
+        };
+        self.status(st)
+    }
+
     /// The decode batch: entry b decodes `slots[b]` starting from `first_tokens[b]`.
     pub fn decode_setup(&mut self, slots: &[i32], first_tokens: &[u32]) -> Result<(), String> {
         if slots.len() != first_tokens.len() {

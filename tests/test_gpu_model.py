@@ -421,3 +421,47 @@ def test_device_sampling_matches_reference_rule(plane, temperature, top_k):
     g1 = gm.generate(p, 8)
     om, _ = _pair(plane, cfg, seed=71)
     assert np.array_equal(g1, om.generate(p, 8))
+
+
+@pytest.mark.parametrize("kv_f16,max_tokens", [(False, 64), (True, 64), (True, 48), (False, 16)])
+def test_batch_prefill_vs_oracle(plane, kv_f16, max_tokens):
+    """Several prompts prefilled in one pass (bh_model_prefill_batch: with an fp16 cache every
+    sequence padded to whole 16-row groups with pad rows that write no KV row; chunks of at most
+    max_tokens rows cutting through sequences), then decoded together: every sequence's ids and
+    logits as the oracle's own prefill + decode of it (f32 cache: the 1e-4 bar; fp16 cache: the
+    fp16 bars with the tie rule). Prompt lengths 1 (nothing to prefill), 6, 21, 40 and 17."""
+    cfg = tiny_cfg(Q4_G32, Q4_G32, gqa7=True, max_seqs=5, kv_rows=5 * 128, kv_f16=kv_f16, max_tokens=max_tokens)
+    om, gm = _pair(plane, cfg, seed=61)
+    lens = [1, 6, 21, 40, 17]
+    prompts = [prompt(n, cfg.vocab, seed=400 + s) for s, n in enumerate(lens)]
+    slots = [3, 0, 4, 1, 2]
+    for s in slots:
+        gm.seq_open(s, 128)
+    gm.prefill_batch(slots, [p[:-1] for p in prompts])
+    gm.decode_setup(slots, [p[-1] for p in prompts])
+    ids, lg = gm.decode(8, want_logits=True)
+    for b, p in enumerate(prompts):
+        want, wl = om.generate(p, 8, want_logits=True)
+        n = len(want)
+        if not kv_f16:
+            assert np.array_equal(ids[:n, b], want), b
+            assert np.max(np.abs(lg[:n, b] - wl)) <= 1e-4 * max(1.0, np.abs(wl).max()), b
+        else:
+            k = agreement(want, list(ids[:n, b]), wl, lg[:n, b])
+            assert k == n, b
+            assert np.max(np.abs(wl[:k] - lg[:k, b])) < 2e-2 and max(rel_l2(lg[t, b], wl[t]) for t in range(k)) < 1e-3, b
+
+
+def test_batch_prefill_errors(plane):
+    """A slot twice in one batch, a closed slot and a prompt past the slot's capacity are refused
+    with nothing prefilled; an empty batch is a no-op."""
+    cfg = tiny_cfg(Q4_G32, Q4_G32, max_seqs=3, kv_rows=3 * 64)
+    _, gm = _pair(plane, cfg, seed=3)
+    gm.seq_open(0, 32)
+    gm.seq_open(1, 32)
+    from bramha_amd._lib import BhError
+    for slots, toks in (([0, 0], [[1, 2], [3]]), ([0, 2], [[1], [2]]), ([1], [list(range(40))])):
+        with pytest.raises(BhError):
+            gm.prefill_batch(slots, toks)
+    assert gm.seq_len(0) == 0 and gm.seq_len(1) == 0
+    gm.prefill_batch([], [])

@@ -163,10 +163,12 @@ def test_gemv_ragged_rows(plane, fmt, n, k, batch):
 
 
 @pytest.mark.parametrize("fmt", [BH_Q4_G32, BH_Q4_ROW])
-@pytest.mark.parametrize("n,k,batch", [(896, 896, 64), (896, 896, 257), (4864, 896, 130), (896, 4864, 200), (300, 96, 71)])
+@pytest.mark.parametrize("n,k,batch", [(896, 896, 64), (896, 896, 257), (4864, 896, 130), (896, 4864, 200), (300, 96, 71),
+                                       (896, 896, 600), (18944, 896, 257), (896, 4864, 1031)])
 def test_gemv_prefill_tiles(plane, fmt, n, k, batch):
-    """Token counts of prefill chunks (>= 64): one tiled MFMA launch over all tokens, with ragged
-    row and token tiles."""
+    """Token counts of prefill chunks (>= 64): one tiled MFMA launch over all tokens with ragged
+    row and token tiles where its grid fills the chip (18944 rows; 600 and 1031 tokens), else one
+    launch of up to 32 16-token MFMA groups, with a K split over workgroups for long K."""
     w = _w(fmt * 17 + n + batch, n, k)
     q, s, deq = _quant(fmt, w)
     x = np.random.default_rng(batch).standard_normal((batch, k)).astype(np.float32)
