@@ -73,23 +73,27 @@ enum Epi : int {
 // wavefront is 1 KiB of contiguous bytes (64 lanes x 16 B). kv_k_off / kv_v_off give the
 // offset (in elements, from the head's base h * kv_rows * hd) of element (t, d).
 __host__ __device__ constexpr int KV_TILE(int hd) { return hd == 64 ? 64 : 32; }
+__host__ __device__ constexpr int KV_TILE_SHIFT(int hd) { return hd == 64 ? 6 : 5; }
+static_assert(KV_TILE(64) == 1 << KV_TILE_SHIFT(64) && KV_TILE(128) == 1 << KV_TILE_SHIFT(128), "tile height");
 // K operand (16-row block blk, 32-wide chunk kc of the head dim) of lane (lr, lg) holds row
 // 32(blk/2) + 8(lr/4) + 4(blk%2) + lr%4 of the tile, dims 32kc + 8lg .. +7.
+// (t >= 0, 0 <= d < hd; shifts and masks throughout: a 64-bit division by the run-time tile
+// height cost the epilogues that write KV rows more than their stores.)
 __host__ __device__ inline int64_t kv_k_off(int64_t t, int d, int hd) {
-    const int tr = KV_TILE(hd), kcs = hd / 32;
-    const int r = (int)(t % tr);
-    const int blk = 2 * (r / 32) + (r % 8) / 4, lr = 4 * ((r % 32) / 8) + (r % 4);
-    const int kc = d / 32, lg = (d % 32) / 8;
-    return (t / tr) * (int64_t)tr * hd + ((int64_t)((blk * kcs + kc) * 64 + lr + 16 * lg) * 8 + d % 8);
+    const int ts = KV_TILE_SHIFT(hd), kcs = hd >> 5;
+    const int r = (int)(t & ((1 << ts) - 1));
+    const int blk = 2 * (r >> 5) + ((r & 7) >> 2), lr = 4 * ((r & 31) >> 3) + (r & 3);
+    const int kc = d >> 5, lg = (d & 31) >> 3;
+    return ((t >> ts) << ts) * hd + ((int64_t)((blk * kcs + kc) * 64 + lr + 16 * lg) * 8 + (d & 7));
 }
 // V^T operand (32-row group j, 16-wide dim block db) of lane (lr, lg) holds dim 16db + lr of
 // rows 32j + 8lg .. +7 of the tile.
 __host__ __device__ inline int64_t kv_v_off(int64_t t, int d, int hd) {
-    const int tr = KV_TILE(hd), dbs = hd / 16;
-    const int r = (int)(t % tr);
-    const int j = r / 32, lg = (r % 32) / 8;
-    const int db = d / 16, lr = d % 16;
-    return (t / tr) * (int64_t)tr * hd + ((int64_t)((j * dbs + db) * 64 + lr + 16 * lg) * 8 + r % 8);
+    const int ts = KV_TILE_SHIFT(hd), dbs = hd >> 4;
+    const int r = (int)(t & ((1 << ts) - 1));
+    const int j = r >> 5, lg = (r & 31) >> 3;
+    const int db = d >> 4, lr = d & 15;
+    return ((t >> ts) << ts) * hd + ((int64_t)((j * dbs + db) * 64 + lr + 16 * lg) * 8 + (r & 7));
 }
 struct KvView {
     void* k = nullptr;

@@ -300,6 +300,95 @@ struct ResPre {
     }
 };
 
+// Batched EPI_QKV operands of the elements i = threadIdx.x + k * NT that a thread finishes: NT is
+// a multiple of ROWS, so the thread keeps one row, row0 + threadIdx.x % ROWS, for the tokens
+// threadIdx.x / ROWS + k * NT / ROWS. request() reads each token's position and KV-region offset
+// at kernel start, as scalar loads (a wave's elements share their token); rope() reads the row's
+// biases and each element's RoPE (cos, sin) once the main loop is done. Without them the
+// epilogue walked position -> RoPE table one token at a time: two dependent round trips per
+// element after the split reduction (Qwen2-7B QKV at 16 tokens: ~5 of its 17.6 us).
+template <int B, int ROWS, int NT>
+struct QkvPre {
+    static_assert(NT % ROWS == 0, "a thread finishes one row");
+    static constexpr int PER = (B * ROWS + NT - 1) / NT;
+    int p[PER];
+    int64_t off[PER];
+    float2 cs[PER];
+    float bias = 0.f, pbias = 0.f;
+    __device__ __forceinline__ void request(const GemvArgs& a) {
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int b = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / ROWS) + k * (NT / ROWS));
+            p[k] = -1;
+            off[k] = 0;
+            if (b < B && b < a.batch) {
+                p[k] = a.pos[b];
+                if (a.boff) off[k] = a.boff[b];
+            }
+        }
+    }
+    __device__ __forceinline__ void rope(const GemvArgs& a, int64_t row0) {
+        const int64_t nn = row0 + threadIdx.x % ROWS;
+        const int half = a.hd >> 1;
+        const int sec = nn < a.qd ? 0 : (nn < a.qd + a.kd ? 1 : 2);
+        const int loc = (int)nn - (sec == 0 ? 0 : (sec == 1 ? a.qd : a.qd + a.kd));
+        const int d = loc % a.hd;
+        if (a.bias && nn < a.N) {
+            bias = a.bias[nn];
+            if (sec < 2) pbias = a.bias[nn + (d < half ? half : -half)];
+        }
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            cs[k] = make_float2(1.f, 0.f);
+            if (nn < a.N && sec < 2 && p[k] >= 0) cs[k] = a.rope[(int64_t)p[k] * half + (d < half ? d : d - half)];
+        }
+    }
+};
+
+// run_epilogue's batched EPI_QKV with the operands of QkvPre (same arithmetic and order).
+template <int FMT, int B, int ROWS, int NT>
+__device__ __forceinline__ void run_qkv_pre(const GemvArgs& a, const float* fin, const float* rn, int64_t row0,
+                                            const QkvPre<B, ROWS, NT>& qp) {
+    const int half = a.hd >> 1;
+    const int64_t nn = row0 + threadIdx.x % ROWS;
+    if (nn >= a.N) return;
+    const int sec = nn < a.qd ? 0 : (nn < a.qd + a.kd ? 1 : 2);
+    const int loc = (int)nn - (sec == 0 ? 0 : (sec == 1 ? a.qd : a.qd + a.kd));
+    const int hh = loc / a.hd, d = loc % a.hd;
+    const int dp = d < half ? half : -half;
+#pragma unroll
+    for (int k = 0; k < QkvPre<B, ROWS, NT>::PER; ++k) {
+        const int i = threadIdx.x + k * NT;
+        const int b = i / ROWS;
+        if (i >= B * ROWS || b >= a.batch) continue;
+        float val = fin[i] * row_scale<FMT>(a.S, nn) * rn[b];
+        if (a.bias) val += qp.bias;
+        const int p = qp.p[k];
+        if (p < 0) {  // a pad token of a multi-sequence prefill: no RoPE, no KV row
+            if (sec == 0) a.y[(int64_t)b * a.ldy + nn] = 0.f;
+            continue;
+        }
+        if (sec < 2) {  // rotate-half RoPE (apply_rope_cpu, cpu_engine.rs:1682-1699)
+            float pv = fin[i + dp] * row_scale<FMT>(a.S, nn + dp) * rn[b];
+            if (a.bias) pv += qp.pbias;
+            const float2 cs = qp.cs[k];
+            val = d < half ? (val * cs.x - pv * cs.y) : (val * cs.x + pv * cs.y);
+        }
+        if (sec == 0) {
+            a.y[(int64_t)b * a.ldy + nn] = val;
+        } else {
+            const int64_t row = qp.off[k] + kv_phys_row(a.kv, p);
+            const int64_t head = (int64_t)hh * a.kv.kv_rows * a.hd;
+            if (a.kv.kv_f16) {  // MFMA-tile order (kv_k_off / kv_v_off)
+                if (sec == 1) ((__half*)a.kv.k)[head + kv_k_off(row, d, a.hd)] = __float2half(val);
+                else ((__half*)a.kv.v)[head + kv_v_off(row, d, a.hd)] = __float2half(val);
+            } else {
+                ((float*)(sec == 1 ? a.kv.k : a.kv.v))[head + row * a.hd + d] = val;
+            }
+        }
+    }
+}
+
 // run_epilogue's batched EPI_RESNORM with the operands of ResPre (same arithmetic and order).
 template <int FMT, int B, int ROWS, int NT>
 __device__ __forceinline__ void run_resnorm_pre(const GemvArgs& a, const float* fin, float* scratch, int64_t row0,

@@ -167,6 +167,8 @@ __global__ void __launch_bounds__(64 * KW * RW) k_gemm_mf(const GemvArgs a0) {
     if constexpr (EPI == EPI_LMHEAD) pp.load(a, (int64_t)tile * ROWS);
     ResPre<B, ROWS, NT> rp;  // residual producers: residual, norm weight, bias, likewise
     if constexpr (EPI == EPI_RESNORM) rp.load(a, (int64_t)tile * ROWS);
+    QkvPre<B, ROWS, NT> qp;  // QKV: the tokens' positions and KV offsets (scalar loads)
+    if constexpr (EPI == EPI_QKV) qp.request(a);
     if (c0 < c1) {
         for (int c = c0;; c += 2 * S) {
             fetch(c + S, s1);
@@ -181,6 +183,7 @@ __global__ void __launch_bounds__(64 * KW * RW) k_gemm_mf(const GemvArgs a0) {
     }
 
     rq.finish(a, rn);  // read by the epilogue, after the barriers below
+    if constexpr (EPI == EPI_QKV) qp.rope(a, (int64_t)tile * ROWS);  // in flight through the reduction
     // D layout: lane holds token tb * 16 + lr, rows 4 * lg + v of each 16-row block. In the
     // exchange buffers a token's rows are TS = ROWS + 4 floats apart and row 4 lg + v of a block
     // sits at 4 v + lg, so the 64 lanes of one D element fall in 64 distinct banks (4 lr + lg);
@@ -263,6 +266,8 @@ __global__ void __launch_bounds__(64 * KW * RW) k_gemm_mf(const GemvArgs a0) {
         run_lmhead_pre<FMT, B, ROWS, NT>(a, comb, comb + TOT, rn, (int64_t)tile * ROWS, pp);
     else if constexpr (EPI == EPI_RESNORM)
         run_resnorm_pre<FMT, B, ROWS, NT>(a, comb, comb + TOT, (int64_t)tile * ROWS, rp);
+    else if constexpr (EPI == EPI_QKV)
+        run_qkv_pre<FMT, B, ROWS, NT>(a, comb, rn, (int64_t)tile * ROWS, qp);
     else
         run_epilogue<FMT, B, EPI, ROWS>(a, comb, comb + TOT, rn, (int64_t)tile * ROWS);
 }
