@@ -61,36 +61,12 @@ struct AttnWave {
     KvTile<HD> A, B;
     int wv = 0, nw = NW;  // this wave's index among the waves sharing the range, and their number
 
-    __device__ __forceinline__ void load_tile(KvTile<HD>& T, int t0) const {
+    // The tile at t0 for a sequence whose region is not tile-aligned: rows one by one through
+    // kv_k_off / kv_v_off, rows at or past r1 zero.
+    __device__ __forceinline__ void load_rows(KvTile<HD>& T, int t0) const {
         const int lane = threadIdx.x & 63;
         const int lr = lane & 15, lg = lane >> 4;
         const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
-        const bool part = t0 + TR > r1;  // wave-uniform: rows past r1 are not loaded (stale bytes)
-        if (tiled) {
-            const __half* kb = Kh + (off + t0) * HD;  // the tile's first element
-            const __half* vb = Vh + (off + t0) * HD;
-#pragma unroll
-            for (int blk = 0; blk < NB; ++blk) {
-                const bool ok = !part || t0 + mf_row(blk, lr) < r1;
-#pragma unroll
-                for (int kc = 0; kc < KC; ++kc)
-                    T.k[blk][kc] = ok ? *(const half8*)(kb + ((blk * KC + kc) * 64 + lane) * 8) : zero;
-            }
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-                const int tg = t0 + 32 * j + 8 * lg;  // this lane group's 8 rows
-#pragma unroll
-                for (int db = 0; db < DB; ++db) {
-                    half8 v = (!part || tg < r1) ? *(const half8*)(vb + ((j * DB + db) * 64 + lane) * 8) : zero;
-                    if (part) {
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) v[e] = tg + e < r1 ? v[e] : (_Float16)0.f;
-                    }
-                    T.v[j][db] = v;
-                }
-            }
-            return;
-        }
 #pragma unroll
         for (int blk = 0; blk < NB; ++blk) {
             const int t = t0 + mf_row(blk, lr);
@@ -117,8 +93,16 @@ struct AttnWave {
         }
     }
 
+    // The tile at t0. A tile-aligned region reads the whole tile unconditionally: it lies inside
+    // the cache (the region starts on a 64-row boundary and kv_rows is a multiple of 64); K rows
+    // at or past r1 only give scores that are masked, V rows there are zeroed by compute().
+    __device__ __forceinline__ void load_tile(KvTile<HD>& T, int t0) const {
+        if (tiled) load_full(T, t0);
+        else load_rows(T, t0);
+    }
+
     // The tile at t0 with every row loaded (rows past r1 included: the caller guarantees they
-    // are inside the region); used before r1 is known, then zero_tail clears the V rows past it.
+    // are inside the cache).
     __device__ __forceinline__ void load_full(KvTile<HD>& T, int t0) const {
         const int lane = threadIdx.x & 63;
         const __half* kb = Kh + (off + t0) * HD;
@@ -213,12 +197,15 @@ struct AttnWave {
             }
     }
 
-    __device__ __forceinline__ void compute(const KvTile<HD>& T, int t0, const half8 (&qh)[KC], const half8 (&ql)[KC],
+    __device__ __forceinline__ void compute(KvTile<HD>& T, int t0, const half8 (&qh)[KC], const half8 (&ql)[KC],
                                             float& m, float& l, f32x4 (&o)[DB]) const {
+        if (t0 + TR > r1) zero_tail(T, t0);  // wave-uniform: the rows past r1 a whole-tile load brought
         if (t0 + TR <= lim_all) compute_t<false>(T, t0, qh, ql, m, l, o);  // wave-uniform
         else compute_t<true>(T, t0, qh, ql, m, l, o);
     }
 
+    // The wave's tiles t = r0 + TR wv + k step below r1 (A holds the first on entry), the next
+    // tile's loads in flight while the current one is multiplied.
     __device__ __forceinline__ void run(const half8 (&qh)[KC], const half8 (&ql)[KC], float& m, float& l, f32x4 (&o)[DB]) {
         const int step = nw * TR;
         for (int t = r0 + wv * TR; t < r1;) {

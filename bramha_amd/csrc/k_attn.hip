@@ -350,8 +350,7 @@ __global__ void __launch_bounds__(64 * NW) k_attn_mf(const AttnArgs a) {
     }
     const int r1 = min(len, r0 + a.split_rows);
     aw.r1 = aw.lim = aw.lim_all = r1;
-    if (!spec) aw.start();
-    else if (tfirst < r1 && tfirst + AttnWave<HD, NW, false>::TR > r1) aw.zero_tail(aw.A, tfirst);
+    if (!spec) aw.start();  // (a partial first tile's V rows past r1 are zeroed by compute())
 
     // q rows into LDS, then Q^T as the B operand:
     // lane (lr, lg) holds head lr, head-dim kc*32 + 8lg .. +7

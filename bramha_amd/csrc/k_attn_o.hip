@@ -139,8 +139,7 @@ __global__ void __launch_bounds__(64 * AO_WAVES) k_attn_o(const AttnArgs at, con
         if (at.kv.max_context > 0) len = min(len, at.kv.max_context);
         const int r1 = min(len, at.split_rows);
         aw.r1 = aw.lim = aw.lim_all = r1;
-        if (!spec) aw.start();
-        else if (tfirst < r1 && tfirst + AW::TR > r1) aw.zero_tail(aw.A, tfirst);
+        if (!spec) aw.start();  // (a partial first tile's V rows past r1 are zeroed by compute())
         half8 qh[KC], ql[KC];
 #pragma unroll
         for (int kc = 0; kc < KC; ++kc) split_hl(qv[kc], qh[kc], ql[kc]);
