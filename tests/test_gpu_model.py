@@ -204,6 +204,49 @@ def test_tiny_fp16_kv(plane):
 
 
 @pytest.mark.parametrize("hd128", [False, True])
+@pytest.mark.parametrize("batch", [1, 2])
+def test_fp16_kv_rows_past_the_length_are_never_used(plane, hd128, batch):
+    """Every row of the slots' KV regions is NaN before the prefill, and the rows past each
+    sequence's length stay NaN until the decode writes them. The prefill attention, the batch-1
+    attention + O launch and the batched decode attention load whole KV tiles, rows past the
+    length included: the logits must equal, bit for bit, those of the same model over a
+    zero-filled cache (and agree with the oracle). Prompts of 45 and 29 rows and 21 decode steps
+    end inside tiles."""
+    if hd128:
+        cfg = tiny_cfg(Q4_G32, Q4_G32, kv_f16=True, hidden=512, n_heads=4, n_kv_heads=2, head_dim=128, ffn=768)
+    else:
+        cfg = tiny_cfg(Q4_G32, Q4_G32, gqa7=True, kv_f16=True)
+    w, _ = tiny_weights(cfg, 61 + hd128)
+    om = oracle.OracleModel(cfg)
+    om.load(w)
+    prompts = [prompt(45, cfg.vocab, seed=62), prompt(29, cfg.vocab, seed=63)][:batch]
+    steps, cap = 21, 128
+    runs = []
+    for fill in (np.nan, 0.0):
+        gm = HipDecoder(plane, cfg)
+        gm.load(w)
+        rows = np.full((cfg.n_layers, cap, cfg.kv_dim), fill, np.float32)
+        for s in range(batch):
+            gm.seq_open(s, cap)
+            gm.kv_write(s, 0, rows, rows)
+            assert gm.seq_len(s) == cap
+            gm.seq_open(s, cap)  # the same region, length 0
+            gm.prefill(s, prompts[s][:-1])
+        gm.decode_setup(list(range(batch)), [int(p[-1]) for p in prompts])
+        runs.append(gm.decode(steps, want_logits=True))
+        gm.close()
+    (gids, glg), (zids, zlg) = runs
+    assert np.all(np.isfinite(glg))
+    assert np.array_equal(gids, zids) and np.array_equal(glg.view(np.uint32), zlg.view(np.uint32))
+    for s in range(batch):
+        oids, olg = om.generate(prompts[s], steps, want_logits=True)
+        n = agreement(oids, gids[:, s], olg, glg[:, s])
+        assert n >= 8, (s, n)
+        assert np.max(np.abs(olg[:n] - glg[:n, s])) < 2e-2
+        assert max(rel_l2(glg[t, s], olg[t]) for t in range(n)) < 1e-3
+
+
+@pytest.mark.parametrize("hd128", [False, True])
 def test_tiny_prefill_tiled_fp16_kv(plane, hd128):
     """A 199-token prefill chunk: tiled MFMA projections over all tokens (QKV with RoPE and KV
     append, O and down with the residual add, gate/up with SiLU) and the causal prefill
