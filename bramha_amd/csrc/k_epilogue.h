@@ -304,9 +304,9 @@ struct ResPre {
 // a multiple of ROWS, so the thread keeps one row, row0 + threadIdx.x % ROWS, for the tokens
 // threadIdx.x / ROWS + k * NT / ROWS. request() reads each token's position and KV-region offset
 // at kernel start, as scalar loads (a wave's elements share their token); rope() reads the row's
-// biases and each element's RoPE (cos, sin) once the main loop is done. Without them the
-// epilogue walked position -> RoPE table one token at a time: two dependent round trips per
-// element after the split reduction (Qwen2-7B QKV at 16 tokens: ~5 of its 17.6 us).
+// biases and each element's RoPE (cos, sin) once the main loop is done, in flight through the
+// split reduction. Without them the epilogue walked position -> RoPE table one token at a time
+// after the reduction (Qwen2-7B QKV at 16 tokens: 17.6 -> 16.8 us).
 template <int B, int ROWS, int NT>
 struct QkvPre {
     static_assert(NT % ROWS == 0, "a thread finishes one row");
