@@ -94,6 +94,20 @@ def launch_floor(plane, n=896, iters=200):
     return out
 
 
+def grid_barrier(plane, iters=20):
+    """Time per phase of a persistent grid of 14 to 256 resident workgroups whose phases (the
+    chain link's work) are separated by a grid-wide barrier with release/acquire ordering
+    (bh_time_probe mode 3): what fusing the decode step's dependent launches into one persistent
+    kernel would pay per boundary instead of the dependent-launch floor."""
+    from bramha_amd import ops
+
+    out = {}
+    for wgs in (14, 36, 112, 256):
+        out[str(wgs)] = round(ops.time_probe(plane, 3, 4096, wgs, 4, iters=iters), 3)
+    log("grid barrier (us per phase at 14 / 36 / 112 / 256 resident workgroups): %s" % out)
+    return out
+
+
 def above_floor(roof, floor):
     """Per kernel class: mean launch time minus the dependent-launch floor, and the step's
     launch count times that floor (the floor of the 256-workgroup chain, the largest of the
@@ -552,6 +566,7 @@ def main():
     log("bs1: %.1f tok/s (%.3f ms/step)" % (tok1, dt1 * 1e3 / args.steps))
     kern, roof = roofline(m1, batch=1)
     roof["floor"] = above_floor(roof, floor)
+    roof["floor"]["grid_barrier_us_by_workgroups"] = grid_barrier(plane)
     log("dominant kernel %s: %.1f GB/s (%.1f%% of HBM peak)" % (kern, roof["achieved"], 100 * roof["frac"]))
     log("bs1 time above the dependent-launch floor: %s" % roof["floor"])
     m1.close()

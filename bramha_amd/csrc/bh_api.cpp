@@ -813,10 +813,34 @@ int bh_time_gemv(bh_ctx* ctx, const bh_weight* wh, const float* x, float* y, int
 }
 
 int bh_time_probe(bh_ctx* ctx, int copy, size_t bytes, int wgs, int unroll, int iters, double* us_per_launch) {
-    if (!ctx || bytes < 16 || wgs <= 0 || wgs > (1 << 20) || iters <= 0 || !us_per_launch || copy < 0 || copy > 2 ||
+    if (!ctx || bytes < 16 || wgs <= 0 || wgs > (1 << 20) || iters <= 0 || !us_per_launch || copy < 0 || copy > 3 ||
         !(unroll == 4 || unroll == 8 || unroll == 16) || (copy == 2 && bytes > (64u << 20)))
         return BH_ERR_INVALID;
     std::lock_guard<std::mutex> g(ctx->mu);
+    if (copy == 3) {  // grid barriers: time per barrier phase, the grid resident at once
+        int dev = 0, cus = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return ctx->hip_fail(e, "device attributes");
+        if (wgs > cus) return ctx->fail(BH_ERR_INVALID, "grid-barrier probe: at most one workgroup per CU");
+        int* cnt = nullptr;  // [2] counts, then [1] error count, then the data
+        e = hipMalloc(&cnt, 16 + (size_t)gridbar_phases() * wgs * 4);
+        if (e == hipSuccess) e = hipMemset(cnt, 0, 16);
+        int rc = e == hipSuccess ? BH_OK : ctx->hip_fail(e, "hipMalloc(probe buffers)");
+        if (rc == BH_OK)
+            rc = time_graph(ctx, iters, [&](int, hipStream_t st) {
+                return launch_gridbar_probe(cnt, (float*)(cnt + 4), cnt + 2, wgs, st);
+            }, us_per_launch);
+        int bad = 0;
+        if (rc == BH_OK) {
+            e = hipMemcpy(&bad, cnt + 2, 4, hipMemcpyDeviceToHost);
+            if (e != hipSuccess) rc = ctx->hip_fail(e, "hipMemcpy");
+        }
+        if (cnt) hipFree(cnt);
+        if (rc == BH_OK && bad) rc = ctx->fail(BH_ERR_HIP, "grid-barrier probe: a wait gave up");
+        if (rc == BH_OK) *us_per_launch /= gridbar_phases();
+        return rc;
+    }
     bytes &= ~(size_t)15;
     void *src = nullptr, *dst = nullptr, *sink = nullptr;
     hipError_t e = hipMalloc(&src, bytes);

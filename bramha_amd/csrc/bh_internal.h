@@ -330,6 +330,9 @@ hipError_t launch_attn_o(int fmt, const AttnArgs& at, const GemvArgs& o, hipStre
 // wgs workgroups of 256 threads, `unroll` (4, 8, 16) loads in flight per thread.
 hipError_t launch_probe(int copy, const void* src, void* dst, int64_t bytes, int wgs, int unroll, uint32_t* sink,
                         hipStream_t st);
+// Grid-barrier probe: gridbar_phases() barriers over wgs resident workgroups in one launch.
+int gridbar_phases();
+hipError_t launch_gridbar_probe(int* cnt, float* data, int* err, int wgs, hipStream_t st);
 
 // ---------------------------------------------------------------------------
 // Host helpers (bh_host.cpp)

@@ -60,7 +60,60 @@ __global__ void __launch_bounds__(256) k_chain_probe(const float* __restrict__ s
         for (int i = threadIdx.x; i < n; i += 256) dst[i] = src[i] + (v == 1.0e30f ? 1.f : 0.f);
 }
 
+// Grid-barrier probe: GB_PHASES phases in one launch, each the chain link's work (read what
+// another workgroup wrote in the previous phase, write this workgroup's value) followed by a
+// barrier over the whole grid (one arrival count incremented with release ordering, polled with
+// acquire loads), as a persistent kernel would separate the steps of a decode layer. Its time per
+// phase is what such a kernel would pay where the decode step pays a dependent launch. Every wait
+// is bounded: a workgroup that polls GB_SPIN times stops and counts itself in *err (the host
+// launches at most one workgroup per CU, so the grid is resident at once and no wait should end
+// that way).
+constexpr int GB_PHASES = 64;
+constexpr int GB_SPIN = 1 << 21;
+__global__ void __launch_bounds__(256) k_gridbar_probe(int* cnt, float* data, int* err) {
+    const int nwg = gridDim.x, wg = blockIdx.x;
+    __shared__ int s_bad;
+    if (threadIdx.x == 0) s_bad = 0;
+    __syncthreads();
+    for (int p = 0; p < GB_PHASES; ++p) {
+        if (threadIdx.x == 0) {
+            const float v = p ? data[(p - 1) * nwg + (wg + 1) % nwg] : 0.f;
+            data[p * nwg + wg] = v + 1.f;
+            __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+            int spins = 0;
+            while (__hip_atomic_load(cnt, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < (p + 1) * nwg) {
+                if (++spins > GB_SPIN) {
+                    s_bad = 1;
+                    break;
+                }
+            }
+        }
+        __syncthreads();
+        if (s_bad) {
+            if (threadIdx.x == 0) atomicAdd(err, 1);
+            return;
+        }
+    }
+    // the last workgroup to finish polling zeroes the counts for the next launch (cnt[1] counts
+    // the workgroups done with cnt[0])
+    if (threadIdx.x == 0 && __hip_atomic_fetch_add(cnt + 1, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == nwg - 1) {
+        __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(cnt + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 }  // namespace
+
+int gridbar_phases() { return GB_PHASES; }
+
+// One grid-barrier probe launch over wgs workgroups (cnt: two counts, zero before the first
+// launch and left at zero by every launch; data: GB_PHASES * wgs floats; err: the count of
+// workgroups whose wait gave up). The caller keeps wgs at most the device's CU count.
+hipError_t launch_gridbar_probe(int* cnt, float* data, int* err, int wgs, hipStream_t st) {
+    if (!cnt || !data || !err || wgs <= 0) return hipErrorInvalidValue;
+    launch_kernel(k_gridbar_probe, dim3((unsigned)wgs), dim3(256), 0, st, cnt, data, err);
+    return hipGetLastError();
+}
 
 // One probe launch: copy = 0 reads src (sink holds wgs * 256 words), copy = 1 copies src to dst,
 // copy = 2 is one link of the dependent chain (bytes / 4 floats from src to dst).

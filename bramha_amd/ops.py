@@ -174,8 +174,9 @@ def synchronize(plane):
 def time_probe(plane, copy, nbytes, wgs, unroll, iters=20):
     """Mean microseconds of one probe launch (bh_time_probe): copy = False streams nbytes with
     16-byte non-temporal loads, True copies them into a second buffer, 2 is one link of a chain of
-    dependent launches over nbytes / 4 floats."""
+    dependent launches over nbytes / 4 floats, 3 one grid-barrier phase of a resident grid (the
+    time per phase)."""
     us = ctypes.c_double()
-    mode = 2 if copy == 2 else (1 if copy else 0)
+    mode = copy if copy in (2, 3) else (1 if copy else 0)
     check(lib.bh_time_probe(plane.ctx, mode, nbytes, wgs, unroll, iters, ctypes.byref(us)), plane.ctx)
     return us.value

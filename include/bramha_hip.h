@@ -183,7 +183,11 @@ int bh_time_attn(bh_ctx* ctx, const float* q, const void* k, const void* v, int 
  * bandwidth is bytes (2 * bytes) / time. copy = 2 times a chain of dependent launches instead:
  * each of its wgs workgroups reads the bytes / 4 floats the previous launch wrote (workgroup 0
  * writes the next), replayed as a graph like the decode step, so the time per launch is the floor
- * of one dependent decode kernel. The buffers are allocated and freed by the call. */
+ * of one dependent decode kernel. copy = 3 times grid barriers instead: one launch of wgs (at most
+ * the CU count) resident workgroups that run 64 phases of the chain's work, each ended by a barrier
+ * over the grid (an arrival count with release ordering polled with acquire loads, every wait
+ * bounded); the result is the time per phase, to compare with a dependent launch (bytes and
+ * unroll are checked but unused). The buffers are allocated and freed by the call. */
 int bh_time_probe(bh_ctx* ctx, int copy, size_t bytes, int wgs, int unroll, int iters, double* us_per_launch);
 
 /* ------------------------------------------------------------ decoder model */

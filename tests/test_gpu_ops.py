@@ -356,3 +356,14 @@ def test_attention_on_two_streams_keeps_split_scratch_apart(plane):
             assert np.array_equal(outs[i][r].numpy(), want[i]), (i, r)
     for s in streams:
         assert hip.hipStreamDestroy(s) == 0
+
+
+def test_probes_run_and_reject_bad_shapes(plane):
+    """The measurement probes behind the bench's floor figures: a dependent-launch chain link and a
+    grid-barrier phase over a resident grid (every wait bounded; a wait that gave up would fail the
+    call) both time, and a grid-barrier probe wider than one workgroup per CU is refused."""
+    assert ops.time_probe(plane, 2, 896 * 4, 14, 4, iters=8) > 0
+    for wgs in (1, 14, 256):
+        assert ops.time_probe(plane, 3, 4096, wgs, 4, iters=4) > 0
+    with pytest.raises(BhError):
+        ops.time_probe(plane, 3, 4096, 1 << 16, 4, iters=1)
