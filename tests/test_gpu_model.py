@@ -179,6 +179,30 @@ def test_tiny_sink_eviction(plane):
     assert np.max(np.abs(olg - glg)) <= 1e-4 * max(1.0, np.abs(olg).max())
 
 
+def test_batch16_fp16_kv_sink_eviction(plane):
+    """Sixteen sequences decoded together past a 16-row context with 4 sink rows: the KV rows of
+    the 16-token MFMA passes' QKV epilogue land in the ring (positions 4 + (p - 4) % 12), and the
+    batched attention reads each sequence's ring, against the oracle's eviction per sequence.
+    Prompts of 3 to 12 tokens (the reference's prefill stays below the limit), 24 steps."""
+    cfg = tiny_cfg(Q4_G32, Q4_G32, gqa7=True, kv_f16=True, max_context=16, sink_tokens=4, max_seqs=16,
+                   kv_rows=16 * 64)
+    om, gm = _pair(plane, cfg, seed=71)
+    prompts = [prompt(3 + (s * 5) % 10, cfg.vocab, seed=500 + s) for s in range(16)]
+    for s, p in enumerate(prompts):
+        gm.seq_open(s, 64)
+        gm.prefill(s, p[:-1])
+    steps = 24
+    gm.decode_setup(list(range(16)), [int(p[-1]) for p in prompts])
+    ids, lg = gm.decode(steps, want_logits=True)
+    assert np.isfinite(lg).all()
+    for s, p in enumerate(prompts):
+        oids, olg = om.generate(p, steps, want_logits=True)
+        n = agreement(oids, ids[:, s], olg, lg[:, s])
+        assert n >= 12, (s, n)  # well past the first eviction (step 16 - len(p) + 1 at most)
+        assert np.max(np.abs(olg[:n] - lg[:n, s])) < 2e-2, s
+        assert max(rel_l2(lg[t, s], olg[t]) for t in range(n)) < 1e-3, s
+
+
 def test_tiny_fp16_kv_sink_eviction_o_bias(plane):
     """Batch-1 decode over an fp16 cache (attention, O projection and residual add in one
     launch) with sink eviction (a 16-row ring after 4 sink rows) and an O bias."""
