@@ -205,19 +205,30 @@ struct AttnWave {
     }
 
     // The wave's tiles t = r0 + TR wv + k step below r1 (A holds the first on entry), the next
-    // tile's loads in flight while the current one is multiplied.
-    __device__ __forceinline__ void run(const half8 (&qh)[KC], const half8 (&ql)[KC], float& m, float& l, f32x4 (&o)[DB]) {
+    // tile's loads in flight while the current one is multiplied. Loads under a condition leave
+    // the compiler unable to count them, and it then waits for every load in flight before each
+    // tile, the prefetch included; so a wave with a run of three or more whole tiles requests the
+    // next tile unconditionally (past its last tile it re-reads the current one: one tile of
+    // extra reads per wave, which costs more than it saves on runs of one or two tiles).
+    template <bool PIPE>
+    __device__ __forceinline__ void run_t(const half8 (&qh)[KC], const half8 (&ql)[KC], float& m, float& l, f32x4 (&o)[DB]) {
         const int step = nw * TR;
         for (int t = r0 + wv * TR; t < r1;) {
             const int t2 = t + step;
-            if (t2 < r1) load_tile(B, t2);
+            if constexpr (PIPE) load_full(B, t2 < r1 ? t2 : t);
+            else if (t2 < r1) load_tile(B, t2);
             compute(A, t, qh, ql, m, l, o);
             if (t2 >= r1) break;
             const int t3 = t2 + step;
-            if (t3 < r1) load_tile(A, t3);
+            if constexpr (PIPE) load_full(A, t3 < r1 ? t3 : t2);
+            else if (t3 < r1) load_tile(A, t3);
             compute(B, t2, qh, ql, m, l, o);
             t = t3;
         }
+    }
+    __device__ __forceinline__ void run(const half8 (&qh)[KC], const half8 (&ql)[KC], float& m, float& l, f32x4 (&o)[DB]) {
+        if (tiled && r0 + wv * TR + 2 * nw * TR < r1) run_t<true>(qh, ql, m, l, o);
+        else run_t<false>(qh, ql, m, l, o);
     }
 };
 
