@@ -290,6 +290,26 @@ def test_tiny_prefill_tiled_fp16_kv(plane, hd128):
     assert np.max(np.abs(olg[:n] - glg[:n])) < 2e-2 and max(rel_l2(glg[t], olg[t]) for t in range(n)) < 1e-3
 
 
+@pytest.mark.parametrize("hd128,plen", [(False, 800), (True, 420)])
+def test_tiny_long_prompt_attention_runs(plane, hd128, plen):
+    """Prompts long enough that each wave of the causal prefill attention walks three or more
+    whole KV tiles (the run whose next tile is requested unconditionally), prefilled in 256-token
+    chunks, then decode steps over the same rows: against the oracle."""
+    if hd128:
+        cfg = tiny_cfg(Q4_G32, Q4_G32, kv_f16=True, max_tokens=256, hidden=512, n_heads=4, n_kv_heads=2,
+                       head_dim=128, ffn=768)
+    else:
+        cfg = tiny_cfg(Q4_G32, Q4_G32, gqa7=True, kv_f16=True, max_tokens=256)
+    om, gm = _pair(plane, cfg, seed=81 + hd128)
+    p = prompt(plen, cfg.vocab, seed=82)
+    oids, olg = om.generate(p, 8, want_logits=True)
+    gids, glg = gm.generate(p, 8, want_logits=True)
+    assert np.all(np.isfinite(glg))
+    n = agreement(oids, gids, olg, glg)
+    assert n >= 4, n
+    assert np.max(np.abs(olg[:n] - glg[:n])) < 2e-2 and max(rel_l2(glg[t], olg[t]) for t in range(n)) < 1e-3
+
+
 def test_tiny_untied_lm_head(plane):
     cfg = tiny_cfg(Q4_G32, Q4_G32, gqa7=True, tied=False)
     om, gm = _pair(plane, cfg, seed=41)
